@@ -1,0 +1,98 @@
+"""ctypes binding of ``libgdn.so`` (the gfx950 C ABI declared in include/gdn.h).
+
+The library is built in-tree by ``avelang_amd.build``.  There is no
+fallback: if the library is missing or fails to load, every operator
+raises.  ``torch`` is imported first so that the library binds to the HIP
+runtime torch already loaded (one runtime, one device context per process).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime before libgdn.so)
+
+LIB_PATH = Path(__file__).resolve().parent / "libgdn.so"
+
+# Entry points declared in include/gdn.h; tests check every one is exported.
+EXPORTS = (
+    "gdn_chunk_fwd",
+    "gdn_chunk_workspace_bytes",
+    "gdn_recurrent_fwd",
+    "gdn_last_error",
+    "gdn_abi_version",
+)
+
+GDN_OK = 0
+GDN_ERR_NULL = -1
+GDN_ERR_SHAPE = -2
+GDN_ERR_SEQLENS = -3
+GDN_ERR_WORKSPACE = -4
+GDN_ERR_ALIAS = -5
+
+_lock = threading.Lock()
+_lib = None
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+
+class NativeLibraryError(RuntimeError):
+    """libgdn.so is missing or cannot be loaded."""
+
+
+def lib():
+    """Load (once) and return the ctypes handle of libgdn.so."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise NativeLibraryError(
+                f"{LIB_PATH} is not built; run `python -m avelang_amd.build` "
+                "(there is no CPU fallback for the GDN operators)")
+        try:
+            h = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:  # pragma: no cover - environment specific
+            raise NativeLibraryError(f"cannot load {LIB_PATH}: {exc}") from exc
+        h.gdn_chunk_fwd.restype = _i
+        h.gdn_chunk_fwd.argtypes = [
+            _vp, _vp, _vp, _vp, _vp,          # q k v g beta
+            _vp, _vp, _vp, _vp,               # h0 ht o cu_seqlens
+            _i, _i, _i, _i, _i, _i, _i,       # B T Hqk Hv K V N
+            _f, _i, _vp, _sz, _vp,            # scale l2norm ws ws_bytes stream
+        ]
+        h.gdn_chunk_workspace_bytes.restype = _sz
+        h.gdn_chunk_workspace_bytes.argtypes = [_i] * 9
+        h.gdn_recurrent_fwd.restype = _i
+        h.gdn_recurrent_fwd.argtypes = [
+            _vp, _vp, _vp, _vp, _vp,
+            _vp, _vp, _vp, _vp,
+            _i, _i, _i, _i, _i, _i, _i,
+            _f, _i, _vp,
+        ]
+        h.gdn_last_error.restype = ctypes.c_char_p
+        h.gdn_last_error.argtypes = []
+        h.gdn_abi_version.restype = _i
+        h.gdn_abi_version.argtypes = []
+        _lib = h
+        return _lib
+
+
+def last_error() -> str:
+    return lib().gdn_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero ABI return code (ValueError for argument errors)."""
+    if rc == GDN_OK:
+        return
+    msg = last_error()
+    if rc < 0:
+        raise ValueError(f"{what}: {msg} (code {rc})")
+    raise RuntimeError(f"{what}: {msg} (hipError {rc})")

@@ -1,0 +1,642 @@
+// Chunked gated-delta-rule prefill for gfx950 (chunk = 64 tokens).
+//
+// Operator semantics: transformers modeling_qwen3_next.py:374-453
+// (torch_chunk_gated_delta_rule); the reference repository has no GDN code,
+// its launcher convention is python/avelang/backends/amdgpu/driver.py:324-343.
+//
+// Per chunk c of one sequence and v-head h (rows i, j in [0, 64)):
+//   G     = cumsum(g)                  Gam_ij = exp(G_i - G_j), i >= j
+//   A     = strict_lower(diag(beta) K K^T * Gam)
+//   Tb    = (I + A)^-1 diag(beta)
+//   P     = scale * lower_incl(Q K^T * Gam)
+// and, carried across chunks with the fp32 state S [K][V]:
+//   Y     = V - e^G * (K S)            (so vnew = u - w S = Tb Y)
+//   vnew  = Tb Y
+//   o     = scale * e^G * (Q S) + P vnew
+//   S     = e^G_L S + K^T (e^(G_L - G) * vnew)
+//
+// Three launches:
+//   chunk_table_kernel  sequence -> first-chunk offsets (varlen plumbing)
+//   chunk_prep_kernel   one workgroup per (chunk, v-head), fully parallel:
+//                       K K^T and Q K^T on MFMA, blocked UT inverse in fp32,
+//                       Tb (as bf16 hi+lo) and P (bf16) written as ready-made
+//                       MFMA A-operand fragments
+//   chunk_chain_kernel  one workgroup per (sequence, v-head, 16-column V
+//                       tile), sequential over that sequence's chunks; the
+//                       fp32 state slice lives in VGPRs for the whole sequence
+//                       and every product is a 16x16x32 bf16 MFMA.
+// Precision: the three products that feed the state (K S, Tb Y, K^T U) use
+// hi+lo bf16 splits of their fp32 operand(s); Q S and P vnew (output only)
+// use single bf16.
+#include "gdn_common.h"
+
+namespace gdn {
+
+// ---------------------------------------------------------------- layout --
+struct ChunkWs {
+  int32_t* off;     // [N+1] first global chunk of each sequence
+  float* gcum;      // [NC][Hv][64] within-chunk cumulative log-decay
+  u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
+  u16x8* pfrag;     // [NC][Hv][4][2][64]
+  uint16_t* qn;     // l2-normalised copies (only with use_qk_l2norm)
+  uint16_t* kn;
+};
+
+__device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int total,
+                                           int& s, int& e) {
+  if (cu) {
+    s = min(max(cu[n], 0), total);
+    e = min(max(cu[n + 1], s), total);
+  } else {
+    s = n * T;
+    e = s + T;
+  }
+}
+
+// ------------------------------------------------------------- l2norm ----
+// y = bf16(x * rsqrt(sum x^2 + 1e-6)) per row of K; one wavefront per row.
+template <int K>
+__global__ __launch_bounds__(256) void l2norm_rows_kernel(const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y,
+                                                          long long rows) {
+  constexpr int PER = K / 64;
+  const long long row = (long long)blockIdx.x * 4 + threadIdx.x / 64;
+  if (row >= rows) return;
+  const int lane = threadIdx.x % 64;
+  const uint16_t* xr = x + row * K + lane * PER;
+  float vals[PER];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    vals[i] = bf2f(xr[i]);
+    ss += vals[i] * vals[i];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off /= 2) ss += __shfl_xor(ss, off);
+  const float inv = rsqrtf(ss + 1e-6f);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) y[row * K + lane * PER + i] = f2bf(vals[i] * inv);
+}
+
+// -------------------------------------------------------- chunk table ----
+__global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restrict__ cu,
+                                                          int N, int T, int total,
+                                                          int ncmax, int32_t* __restrict__ off) {
+  __shared__ int part[257];
+  const int tid = threadIdx.x;
+  const int per = (N + 255) / 256;
+  const int a = min(tid * per, N), b = min(a + per, N);
+  int sum = 0;
+  for (int n = a; n < b; ++n) {
+    int s, e;
+    seq_bounds(cu, n, T, total, s, e);
+    sum += (e - s + kChunk - 1) / kChunk;
+  }
+  part[tid + 1] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    part[0] = 0;
+    for (int i = 1; i <= 256; ++i) part[i] += part[i - 1];
+  }
+  __syncthreads();
+  int run = part[tid];
+  for (int n = a; n < b; ++n) {
+    off[n] = min(run, ncmax);
+    int s, e;
+    seq_bounds(cu, n, T, total, s, e);
+    run += (e - s + kChunk - 1) / kChunk;
+  }
+  if (tid == 255) off[N] = min(part[256], ncmax);
+}
+
+// ---------------------------------------------------------- prep (K1) ----
+constexpr int kLdA = 68;   // fp32 row stride of A / Tm in LDS
+constexpr int kLdP = 72;   // bf16 row stride of P in LDS
+constexpr int kLdM = 17;
+
+// acc[r] += sum_k X[(4*grp + r) * ldx + k] * Y[k * ldy + c]   (16x16x16, fp32)
+__device__ __forceinline__ void blk_mm(float acc[4], const float* X, int ldx, const float* Y,
+                                       int ldy, int c, int grp) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float y = Y[k * ldy + c];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] += X[(4 * grp + r) * ldx + k] * y;
+  }
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void chunk_prep_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const float* __restrict__ g, const float* __restrict__ beta,
+    const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, float scale,
+    ChunkWs ws) {
+  constexpr int LDK = K + 8;
+  constexpr int KB = K / 32;
+  constexpr int kPhase1 = 2 * 64 * LDK * 2;
+  constexpr int kPhase2 = 2 * 64 * kLdA * 4 + 64 * kLdP * 2 + 4 * 16 * kLdM * 4;
+  constexpr int kBytes = kPhase1 > kPhase2 ? kPhase1 : kPhase2;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kBytes];
+  __shared__ float Gs[64], Bs[64];
+
+  const int ci = blockIdx.x;
+  const int h = blockIdx.y;
+  const int32_t* off = ws.off;
+  if (ci >= off[N]) return;
+  // sequence owning chunk ci: largest n < N with off[n] <= ci
+  int lo = 0, hi = N;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (off[mid] <= ci) lo = mid; else hi = mid;
+  }
+  const int n = lo;
+  int s, e;
+  seq_bounds(cu, n, T, total, s, e);
+  const int t0 = s + (ci - off[n]) * kChunk;
+  const int L = min(kChunk, e - t0);
+  const int hq = h / (Hv / Hqk);
+
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const int r16 = lane % 16, grp = lane / 16;
+
+  // gates: inclusive scan of g (padding rows contribute 0)
+  if (w == 0) {
+    float gv = 0.f, bv = 0.f;
+    if (lane < L) {
+      gv = g[(size_t)(t0 + lane) * Hv + h];
+      bv = beta[(size_t)(t0 + lane) * Hv + h];
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d *= 2) {
+      const float o = __shfl_up(gv, d);
+      if (lane >= d) gv += o;
+    }
+    Gs[lane] = gv;
+    Bs[lane] = bv;
+    ws.gcum[((size_t)ci * Hv + h) * 64 + lane] = gv;
+  }
+
+  // stage K and Q rows of the chunk
+  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* Qs = Ks + 64 * LDK;
+  for (int idx = tid; idx < 64 * (K / 8); idx += 256) {
+    const int row = idx / (K / 8), vec = idx % (K / 8);
+    u16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0}, qv = kv;
+    if (row < L) {
+      const size_t src = ((size_t)(t0 + row) * Hqk + hq) * K + vec * 8;
+      kv = *reinterpret_cast<const u16x8*>(k + src);
+      qv = *reinterpret_cast<const u16x8*>(q + src);
+    }
+    *reinterpret_cast<u16x8*>(Ks + row * LDK + vec * 8) = kv;
+    *reinterpret_cast<u16x8*>(Qs + row * LDK + vec * 8) = qv;
+  }
+  __syncthreads();
+
+  // K K^T and Q K^T for row tile w, column tiles <= w
+  f32x4 kk[4], qk[4];
+#pragma unroll
+  for (int tc = 0; tc < 4; ++tc) {
+    kk[tc] = zero4();
+    qk[tc] = zero4();
+    if (tc <= w) {
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        const u16x8 bk = *reinterpret_cast<const u16x8*>(Ks + (16 * tc + r16) * LDK + 32 * b + 8 * grp);
+        const u16x8 ak = *reinterpret_cast<const u16x8*>(Ks + (16 * w + r16) * LDK + 32 * b + 8 * grp);
+        const u16x8 aq = *reinterpret_cast<const u16x8*>(Qs + (16 * w + r16) * LDK + 32 * b + 8 * grp);
+        kk[tc] = mfma16(ak, bk, kk[tc]);
+        qk[tc] = mfma16(aq, bk, qk[tc]);
+      }
+    }
+  }
+  __syncthreads();  // K/Q staging area is reused below
+
+  float* Af = reinterpret_cast<float*>(smem);
+  float* Tm = Af + 64 * kLdA;
+  uint16_t* Ps = reinterpret_cast<uint16_t*>(Tm + 64 * kLdA);
+  float* Msc = reinterpret_cast<float*>(Ps + 64 * kLdP);
+
+#pragma unroll
+  for (int tc = 0; tc < 4; ++tc) {
+    const int j = 16 * tc + r16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * w + 4 * grp + r;
+      float a = 0.f, p = 0.f;
+      if (tc <= w && j <= i) {
+        const float gam = __expf(Gs[i] - Gs[j]);
+        p = scale * qk[tc][r] * gam;
+        if (j < i) a = Bs[i] * kk[tc][r] * gam;
+      }
+      if (tc <= w) Af[i * kLdA + j] = a;
+      Ps[i * kLdP + j] = f2bf(p);
+    }
+  }
+  __syncthreads();
+
+  // (I + A)^-1, blocked by 16: diagonal blocks by forward substitution
+  if (lane < 16) {
+    const float* Ab = Af + 16 * w * kLdA + 16 * w;
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = (i == lane) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) acc -= Ab[i * kLdA + j] * t[j];
+      t[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Tm[(16 * w + i) * kLdA + 16 * w + lane] = t[i];
+  }
+  __syncthreads();
+  // off-diagonal blocks by distance d: T_ij = -T_ii * sum_{m=j}^{i-1} A_im T_mj
+#pragma unroll
+  for (int d = 1; d < 4; ++d) {
+    const int bi = w + d, bj = w;
+    const bool act = bi < 4;
+    if (act) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int m = bj; m < bi; ++m)
+        blk_mm(acc, Af + 16 * bi * kLdA + 16 * m, kLdA, Tm + 16 * m * kLdA + 16 * bj, kLdA,
+               r16, grp);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Msc[(w * 16 + 4 * grp + r) * kLdM + r16] = acc[r];
+    }
+    __syncthreads();
+    if (act) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      blk_mm(acc, Tm + 16 * bi * kLdA + 16 * bi, kLdA, Msc + w * 16 * kLdM, kLdM, r16, grp);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tm[(16 * bi + 4 * grp + r) * kLdA + 16 * bj + r16] = -acc[r];
+    }
+    __syncthreads();
+  }
+
+  // A-operand fragments: row 16w + r16, k = 32b + 8grp + ii
+  const size_t base = ((size_t)ci * Hv + h) * 4 + w;
+  const int row = 16 * w + r16;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    u16x8 th, tl, pf;
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) {
+      const int col = 32 * b + 8 * grp + ii;
+      const float x = (col <= row) ? Tm[row * kLdA + col] * Bs[col] : 0.f;
+      uint16_t xh, xl;
+      split_bf(x, xh, xl);
+      th[ii] = xh;
+      tl[ii] = xl;
+      pf[ii] = Ps[row * kLdP + col];
+    }
+    ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + lane] = th;
+    ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
+    ws.pfrag[(base * 2 + b) * 64 + lane] = pf;
+  }
+}
+
+// --------------------------------------------------------- chain (K2) ----
+template <int K>
+struct ChainIn {
+  static constexpr int KB = K / 32;
+  u16x8 kf[KB], qf[KB];
+  u16x8 tf[2][2];
+  u16x8 pf[2];
+  float vv[4];
+  f32x4 gg;
+  float gl;
+};
+
+template <int K>
+__device__ __forceinline__ void chain_load(ChainIn<K>& in, const uint16_t* __restrict__ q,
+                                           const uint16_t* __restrict__ k,
+                                           const uint16_t* __restrict__ v, const ChunkWs& ws,
+                                           int ci, int t0, int L, int h, int hq, int Hqk,
+                                           int Hv, int V, int vt, int w, int lane) {
+  constexpr int KB = K / 32;
+  const int r16 = lane % 16, grp = lane / 16;
+  const int arow = 16 * w + r16;
+  const u16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  const size_t qk_off = ((size_t)(t0 + arow) * Hqk + hq) * K + 8 * grp;
+#pragma unroll
+  for (int b = 0; b < KB; ++b) {
+    in.kf[b] = arow < L ? *reinterpret_cast<const u16x8*>(k + qk_off + 32 * b) : z8;
+    in.qf[b] = arow < L ? *reinterpret_cast<const u16x8*>(q + qk_off + 32 * b) : z8;
+  }
+  const size_t base = ((size_t)ci * Hv + h) * 4 + w;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    in.tf[b][0] = ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + lane];
+    in.tf[b][1] = ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane];
+    in.pf[b] = ws.pfrag[(base * 2 + b) * 64 + lane];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 16 * w + 4 * grp + r;
+    in.vv[r] = row < L ? bf2f(v[((size_t)(t0 + row) * Hv + h) * V + 16 * vt + r16]) : 0.f;
+  }
+  const float* gc = ws.gcum + ((size_t)ci * Hv + h) * 64;
+  in.gg = *reinterpret_cast<const f32x4*>(gc + 16 * w + 4 * grp);
+  in.gl = gc[L - 1];
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void chunk_chain_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
+    const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
+    float scale, ChunkWs ws) {
+  constexpr int KB = K / 32;     // k-blocks of K S
+  constexpr int RT = K / 64;     // 16-row state tiles per wave
+  constexpr int LDS_ = K + 8;    // S^T row stride (bf16)
+  constexpr int LDY = 72;        // 64-row operands
+  __shared__ __attribute__((aligned(16))) uint16_t SsT[2][16][LDS_];
+  __shared__ __attribute__((aligned(16))) uint16_t YsT[2][16][LDY];
+  __shared__ __attribute__((aligned(16))) uint16_t UsT[2][16][LDY];
+  __shared__ __attribute__((aligned(16))) uint16_t VnT[16][LDY];
+  __shared__ __attribute__((aligned(16))) uint16_t Kl[64][LDS_];
+
+  const int NVT = V / 16;
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);  // one head's tiles per XCD
+  const int vt = bid % NVT;
+  const int h = (bid / NVT) % Hv;
+  const int n = bid / NVT / Hv;
+  const int hq = h / (Hv / Hqk);
+
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const int r16 = lane % 16, grp = lane / 16;
+
+  int s, e;
+  seq_bounds(cu, n, T, total, s, e);
+  const int c_begin = ws.off[n], c_end = ws.off[n + 1];
+
+  // state slice: rows w*16*RT + 16*tt + 4*grp + r, column 16*vt + r16
+  const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
+  f32x4 Sr[RT];
+#pragma unroll
+  for (int tt = 0; tt < RT; ++tt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
+      Sr[tt][r] = h0 ? h0[tile + (size_t)kd * V] : 0.f;
+    }
+  }
+  auto publish_state = [&]() {
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+      u16x4 hi4, lo4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint16_t a, b;
+        split_bf(Sr[tt][r], a, b);
+        hi4[r] = a;
+        lo4[r] = b;
+      }
+      const int kd0 = w * 16 * RT + 16 * tt + 4 * grp;
+      *reinterpret_cast<u16x4*>(&SsT[0][r16][kd0]) = hi4;
+      *reinterpret_cast<u16x4*>(&SsT[1][r16][kd0]) = lo4;
+    }
+  };
+  publish_state();
+  __syncthreads();
+
+  ChainIn<K> cur;
+  if (c_begin < c_end)
+    chain_load<K>(cur, q, k, v, ws, c_begin, s, min(kChunk, e - s), h, hq, Hqk, Hv, V, vt, w,
+                  lane);
+
+  for (int ci = c_begin; ci < c_end; ++ci) {
+    const int t0 = s + (ci - c_begin) * kChunk;
+    const int L = min(kChunk, e - t0);
+    ChainIn<K> nxt;
+    if (ci + 1 < c_end) {
+      const int t1 = t0 + kChunk;
+      chain_load<K>(nxt, q, k, v, ws, ci + 1, t1, min(kChunk, e - t1), h, hq, Hqk, Hv, V, vt,
+                    w, lane);
+    }
+    // stage this chunk's K rows for the K^T operand of the state update
+#pragma unroll
+    for (int b = 0; b < KB; ++b)
+      *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = cur.kf[b];
+
+    // X = K S (hi+lo), QS = Q S (hi)
+    f32x4 X = zero4(), QS = zero4();
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      const u16x8 sh = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]);
+      const u16x8 sl = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 8 * grp]);
+      X = mfma16(cur.kf[b], sh, X);
+      X = mfma16(cur.kf[b], sl, X);
+      QS = mfma16(cur.qf[b], sh, QS);
+    }
+    float eG[4];
+    {
+      u16x4 yh, yl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        eG[r] = __expf(cur.gg[r]);
+        const float y = cur.vv[r] - eG[r] * X[r];
+        uint16_t a, b;
+        split_bf(y, a, b);
+        yh[r] = a;
+        yl[r] = b;
+      }
+      *reinterpret_cast<u16x4*>(&YsT[0][r16][16 * w + 4 * grp]) = yh;
+      *reinterpret_cast<u16x4*>(&YsT[1][r16][16 * w + 4 * grp]) = yl;
+    }
+    __syncthreads();
+
+    // vnew = Tb Y (3-term hi/lo)
+    f32x4 vn = zero4();
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const u16x8 yh = *reinterpret_cast<const u16x8*>(&YsT[0][r16][32 * b + 8 * grp]);
+      const u16x8 yl = *reinterpret_cast<const u16x8*>(&YsT[1][r16][32 * b + 8 * grp]);
+      vn = mfma16(cur.tf[b][0], yh, vn);
+      vn = mfma16(cur.tf[b][0], yl, vn);
+      vn = mfma16(cur.tf[b][1], yh, vn);
+    }
+    {
+      u16x4 uh, ul, vb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float u = __expf(cur.gl - cur.gg[r]) * vn[r];
+        uint16_t a, b;
+        split_bf(u, a, b);
+        uh[r] = a;
+        ul[r] = b;
+        vb[r] = f2bf(vn[r]);
+      }
+      *reinterpret_cast<u16x4*>(&UsT[0][r16][16 * w + 4 * grp]) = uh;
+      *reinterpret_cast<u16x4*>(&UsT[1][r16][16 * w + 4 * grp]) = ul;
+      *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
+    }
+    __syncthreads();
+
+    // o = scale e^G (Q S) + P vnew
+    {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const u16x8 vb = *reinterpret_cast<const u16x8*>(&VnT[r16][32 * b + 8 * grp]);
+        acc = mfma16(cur.pf[b], vb, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * w + 4 * grp + r;
+        if (row < L)
+          o[((size_t)(t0 + row) * Hv + h) * V + 16 * vt + r16] =
+              f2bf(scale * eG[r] * QS[r] + acc[r]);
+      }
+    }
+    // S = e^G_L S + K^T U   (U hi+lo)
+    {
+      const float egl = __expf(cur.gl);
+      u16x8 uh[2], ul[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        uh[b] = *reinterpret_cast<const u16x8*>(&UsT[0][r16][32 * b + 8 * grp]);
+        ul[b] = *reinterpret_cast<const u16x8*>(&UsT[1][r16][32 * b + 8 * grp]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt) {
+        const int kd = w * 16 * RT + 16 * tt + r16;
+        f32x4 acc = Sr[tt] * egl;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          u16x8 ka;
+#pragma unroll
+          for (int ii = 0; ii < 8; ++ii) ka[ii] = Kl[32 * b + 8 * grp + ii][kd];
+          acc = mfma16(ka, uh[b], acc);
+          acc = mfma16(ka, ul[b], acc);
+        }
+        Sr[tt] = acc;
+      }
+    }
+    publish_state();
+    __syncthreads();
+    if (ci + 1 < c_end) cur = nxt;
+  }
+
+  if (ht) {
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
+        ht[tile + (size_t)kd * V] = Sr[tt][r];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- host ----
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct WsPlan {
+  size_t off, gcum, tfrag, pfrag, qn, kn, total;
+  long long ncmax;
+};
+
+static WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int N, bool has_cu, bool l2) {
+  WsPlan p{};
+  const long long total = (long long)B * T;
+  p.ncmax = has_cu ? (total + 63LL * N) / 64 : (long long)B * ((T + 63) / 64);
+  size_t at = 0;
+  p.off = at;
+  at = align256(at + (size_t)(N + 1) * 4);
+  p.gcum = at;
+  at = align256(at + (size_t)p.ncmax * Hv * 64 * 4);
+  p.tfrag = at;
+  at = align256(at + (size_t)p.ncmax * Hv * 4 * 2 * 2 * 64 * 16);
+  p.pfrag = at;
+  at = align256(at + (size_t)p.ncmax * Hv * 4 * 2 * 64 * 16);
+  p.qn = p.kn = at;
+  if (l2) {
+    p.qn = at;
+    at = align256(at + (size_t)total * Hqk * K * 2);
+    p.kn = at;
+    at = align256(at + (size_t)total * Hqk * K * 2);
+  }
+  p.total = at;
+  return p;
+}
+
+template <int K>
+static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const float* g, const float* beta, const float* h0, float* ht,
+                         uint16_t* o, const int32_t* cu, int B, int T, int Hqk, int Hv, int V,
+                         int N, float scale, bool l2, const WsPlan& p, unsigned char* wsb,
+                         hipStream_t st) {
+  ChunkWs ws;
+  ws.off = reinterpret_cast<int32_t*>(wsb + p.off);
+  ws.gcum = reinterpret_cast<float*>(wsb + p.gcum);
+  ws.tfrag = reinterpret_cast<u16x8*>(wsb + p.tfrag);
+  ws.pfrag = reinterpret_cast<u16x8*>(wsb + p.pfrag);
+  ws.qn = reinterpret_cast<uint16_t*>(wsb + p.qn);
+  ws.kn = reinterpret_cast<uint16_t*>(wsb + p.kn);
+  const int total = B * T;
+  if (l2) {
+    const long long rows = (long long)total * Hqk;
+    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    hipLaunchKernelGGL((l2norm_rows_kernel<K>), dim3(blocks), dim3(256), 0, st, q, ws.qn, rows);
+    hipLaunchKernelGGL((l2norm_rows_kernel<K>), dim3(blocks), dim3(256), 0, st, k, ws.kn, rows);
+    q = ws.qn;
+    k = ws.kn;
+  }
+  hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, st, cu, N, T, total,
+                     (int)p.ncmax, ws.off);
+  if (p.ncmax > 0)
+    hipLaunchKernelGGL((chunk_prep_kernel<K>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0, st, q,
+                       k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws);
+  hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, q, k,
+                     v, h0, ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+}
+
+}  // namespace gdn
+
+namespace gdn_host {
+int validate_common(const void* q, const void* k, const void* v, const float* g,
+                    const float* beta, const float* h0, const float* ht, const void* o,
+                    const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N);
+}
+
+extern "C" size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
+                                            int N, int has_cu_seqlens, int use_qk_l2norm) {
+  (void)V;
+  if (B < 0 || T < 0 || Hqk <= 0 || Hv <= 0 || N < 0 || K <= 0) return 0;
+  return gdn::plan_ws(B, T, Hqk, Hv, K, N, has_cu_seqlens != 0, use_qk_l2norm != 0).total;
+}
+
+extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                             const float* beta, const float* h0, float* ht, void* o,
+                             const int32_t* cu_seqlens, int B, int T, int Hqk, int Hv, int K,
+                             int V, int N, float scale, int use_qk_l2norm, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk, Hv,
+                                     K, V, N);
+  if (rc) return rc;
+  if (N == 0) return GDN_OK;
+  const gdn::WsPlan p =
+      gdn::plan_ws(B, T, Hqk, Hv, K, N, cu_seqlens != nullptr, use_qk_l2norm != 0);
+  if (!workspace || workspace_bytes < p.total)
+    return gdn_host::fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace needs " +
+                                                 std::to_string(p.total) + " bytes, got " +
+                                                 std::to_string(workspace_bytes));
+  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_fwd: problem too large");
+  auto* qq = static_cast<const uint16_t*>(q);
+  auto* kk = static_cast<const uint16_t*>(k);
+  auto* vv = static_cast<const uint16_t*>(v);
+  auto* oo = static_cast<uint16_t*>(o);
+  auto* wsb = static_cast<unsigned char*>(workspace);
+  auto st = static_cast<hipStream_t>(stream);
+  if (K == 128)
+    gdn::launch_chunk<128>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, Hv, V, N,
+                           scale, use_qk_l2norm != 0, p, wsb, st);
+  else
+    gdn::launch_chunk<64>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, Hv, V, N,
+                          scale, use_qk_l2norm != 0, p, wsb, st);
+  return gdn_host::check_launch("gdn_chunk_fwd");
+}

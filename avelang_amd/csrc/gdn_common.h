@@ -1,0 +1,61 @@
+// Shared device helpers for the gfx950 GDN kernels: bf16 packing, the
+// 16x16x32 bf16 MFMA wrapper, and the thread-local error channel of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/gdn.h"
+
+namespace gdn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 64;  // tokens per chunk of the prefill path
+constexpr int kWave = 64;   // CDNA wavefront width
+
+// bf16 <-> fp32 on raw 16-bit patterns.
+__device__ __forceinline__ float bf2f(uint16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Split x into hi + lo bf16 parts with x ~= hi + lo to ~2^-17 relative.
+__device__ __forceinline__ void split_bf(float x, uint16_t& hi, uint16_t& lo) {
+  hi = f2bf(x);
+  lo = f2bf(x - bf2f(hi));
+}
+
+__device__ __forceinline__ bf16x8 as_bf(u16x8 v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// D += A(16x32) * B(32x16), bf16 operands, fp32 accumulate.
+// Operand slot (lane l, element i) carries reduction index kappa(l/16, i);
+// A and B must use the same kappa.  Output: lane l holds D[4*(l/16)+r][l%16].
+__device__ __forceinline__ f32x4 mfma16(u16x8 a, u16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(a), as_bf(b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+}  // namespace gdn
+
+// ---- host side: error channel shared by every entry point -------------
+namespace gdn_host {
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+}  // namespace gdn_host

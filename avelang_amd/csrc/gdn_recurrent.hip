@@ -1,0 +1,194 @@
+// Fused recurrent gated delta rule for gfx950 (decode: one token per
+// sequence; also multi-token / varlen).
+//
+// Operator semantics: transformers modeling_qwen3_next.py:490-501 (the
+// token loop of torch_recurrent_gated_delta_rule); the reference repository
+// has no GDN code, its launcher convention is backends/amdgpu/driver.py:
+// 324-343 (raw pointers + scalars + caller stream).
+//
+// Design: the path is HBM-bound (0.8 flop/B), so there is no MFMA.  One
+// workgroup of 256 lanes owns one (sequence, v-head) state tile S[K][V]
+// (fp32, 64 KiB at K = V = 128).  Each lane holds a float4 column group of
+// K/ROWG rows in VGPRs; the tile is read once with coalesced 16-byte loads
+// (a wavefront covers whole contiguous rows), advanced through every token
+// of the sequence in registers, and written once.  Per token, the two
+// reductions over K (S^T k and S^T q) and the scalars k.q, |k|^2, |q|^2
+// come from one pass over the registers: lane partials, a xor-shuffle
+// across the row groups inside a wavefront, then a 4-way LDS combine.
+// Using the pre-update S,
+//     S' = e^g S + k (x) d,   d = beta (v - e^g S^T k),
+//     o  = scale (e^g S^T q + d (k.q))
+// so the updated tile never has to be re-read.
+#include "gdn_common.h"
+
+namespace gdn {
+
+template <int K, int V>
+__global__ __launch_bounds__(256) void recurrent_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* __restrict__ g,
+    const float* __restrict__ beta, const float* h0, float* ht,
+    uint16_t* __restrict__ o, const int32_t* __restrict__ cu, int T,
+    int total_tokens, int Hqk, int Hv, float scale, int l2norm) {
+  constexpr int COLG = V / 4;          // float4 column groups per row
+  constexpr int ROWG = 256 / COLG;     // row groups
+  constexpr int RPT = K / ROWG;        // rows per lane
+  constexpr int NRED = 11;             // kv[4], sq[4], kq, kk, qq
+  static_assert(ROWG * COLG == 256 && RPT * ROWG == K, "tile shape");
+  static_assert(COLG <= 64 && 64 % COLG == 0, "wave covers whole rows");
+
+  __shared__ float kq_s[2][K];
+  __shared__ float red[4][COLG][NRED + 1];
+
+  const int tid = threadIdx.x;
+  const int cg = tid % COLG;
+  const int rg = tid / COLG;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int h = blockIdx.x % Hv;
+  const int n = blockIdx.x / Hv;
+  const int hq = h / (Hv / Hqk);
+
+  int s, e;
+  if (cu) {
+    s = min(max(cu[n], 0), total_tokens);
+    e = min(max(cu[n + 1], s), total_tokens);
+  } else {
+    s = n * T;
+    e = s + T;
+  }
+
+  const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V;
+  f32x4 S[RPT];
+  if (h0) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(h0 + tile);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      S[i] = __builtin_nontemporal_load(src + (size_t)(rg + ROWG * i) * COLG + cg);
+  } else {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) S[i] = zero4();
+  }
+
+  for (int t = s; t < e; ++t) {
+    const size_t qk_row = ((size_t)t * Hqk + hq) * K;
+    if (tid < K) {
+      kq_s[0][tid] = bf2f(k[qk_row + tid]);
+      kq_s[1][tid] = bf2f(q[qk_row + tid]);
+    }
+    const size_t vh = (size_t)t * Hv + h;
+    const u16x4 vb = *reinterpret_cast<const u16x4*>(v + vh * V + 4 * cg);
+    const float gt = g[vh];
+    const float bt = beta[vh];
+    __syncthreads();
+
+    float r[NRED];
+    float kreg[RPT];  // k rows kept in VGPRs: kq_s is restaged by the next token
+#pragma unroll
+    for (int j = 0; j < NRED; ++j) r[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const float kr = kq_s[0][rg + ROWG * i];
+      const float qr = kq_s[1][rg + ROWG * i];
+      kreg[i] = kr;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        r[c] += S[i][c] * kr;
+        r[4 + c] += S[i][c] * qr;
+      }
+      r[8] += kr * qr;
+      r[9] += kr * kr;
+      r[10] += qr * qr;
+    }
+#pragma unroll
+    for (int off = COLG; off < 64; off *= 2) {
+#pragma unroll
+      for (int j = 0; j < NRED; ++j) r[j] += __shfl_xor(r[j], off);
+    }
+    if (lane < COLG) {
+#pragma unroll
+      for (int j = 0; j < NRED; ++j) red[wave][cg][j] = r[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NRED; ++j)
+      r[j] = red[0][cg][j] + red[1][cg][j] + red[2][cg][j] + red[3][cg][j];
+
+    const float ik = l2norm ? rsqrtf(r[9] + 1e-6f) : 1.f;
+    const float iq = l2norm ? rsqrtf(r[10] + 1e-6f) : 1.f;
+    const float eg = __expf(gt);
+    float d[4];
+    float ov[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      d[c] = bt * (bf2f(vb[c]) - eg * r[c] * ik);
+      ov[c] = scale * iq * (eg * r[4 + c] + d[c] * r[8] * ik);
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const float kr = kreg[i] * ik;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) S[i][c] = eg * S[i][c] + kr * d[c];
+    }
+    if (rg == 0) {
+      u16x4 ob;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ob[c] = f2bf(ov[c]);
+      *reinterpret_cast<u16x4*>(o + vh * V + 4 * cg) = ob;
+    }
+  }
+
+  if (ht) {
+    f32x4* dst = reinterpret_cast<f32x4*>(ht + tile);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      __builtin_nontemporal_store(S[i], dst + (size_t)(rg + ROWG * i) * COLG + cg);
+  }
+}
+
+template <int K, int V>
+static void launch_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             const float* g, const float* beta, const float* h0,
+                             float* ht, uint16_t* o, const int32_t* cu, int B, int T,
+                             int Hqk, int Hv, int N, float scale, int l2norm,
+                             hipStream_t stream) {
+  const int total_tokens = B * T;
+  hipLaunchKernelGGL((recurrent_kernel<K, V>), dim3(N * Hv), dim3(256), 0, stream, q, k, v,
+                     g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm);
+}
+
+}  // namespace gdn
+
+namespace gdn_host {
+int validate_common(const void* q, const void* k, const void* v, const float* g,
+                    const float* beta, const float* h0, const float* ht, const void* o,
+                    const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N);
+}
+
+extern "C" int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
+                                 const float* g, const float* beta, const float* h0,
+                                 float* ht, void* o, const int32_t* cu_seqlens, int B,
+                                 int T, int Hqk, int Hv, int K, int V, int N, float scale,
+                                 int use_qk_l2norm, void* stream) {
+  int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk,
+                                     Hv, K, V, N);
+  if (rc) return rc;
+  if (N == 0 || Hv == 0) return GDN_OK;
+  auto* qq = static_cast<const uint16_t*>(q);
+  auto* kk = static_cast<const uint16_t*>(k);
+  auto* vv = static_cast<const uint16_t*>(v);
+  auto* oo = static_cast<uint16_t*>(o);
+  auto st = static_cast<hipStream_t>(stream);
+#define GDN_REC(KK, VV)                                                                   \
+  if (K == KK && V == VV) {                                                               \
+    gdn::launch_recurrent<KK, VV>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, \
+                                  Hv, N, scale, use_qk_l2norm, st);                       \
+    return gdn_host::check_launch("gdn_recurrent_fwd");                                   \
+  }
+  GDN_REC(128, 128)
+  GDN_REC(64, 64)
+  GDN_REC(128, 64)
+  GDN_REC(64, 128)
+#undef GDN_REC
+  return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd: unsupported K/V");
+}

@@ -1,0 +1,227 @@
+"""Gated delta rule operators for MI355X (gfx950).
+
+Python operator surface of the Qwen3-Next gated-delta-net hot path, in the
+shape of the reference's kernel-library wrappers
+(python/avelang_kernels/amdgpu_gemm.py:458-494): validate dtypes and shapes
+and raise ``ValueError`` before anything is launched, allocate outputs on
+the inputs' device, and launch asynchronously on torch's current stream
+(python/avelang/backends/driver.py:24-30).  The kernels are the hand-written
+HIP code of ``avelang_amd/csrc`` behind the C ABI of ``include/gdn.h``; there
+is no fallback path.
+
+Layouts (FLA / transformers convention, modeling_qwen3_next.py:391-393):
+    q, k  [B, T, Hqk, K]  bf16        v, o  [B, T, Hv, V]  bf16
+    g, beta [B, T, Hv]    fp32        state [N, Hv, K, V]  fp32
+v-head h reads qk-head h // (Hv // Hqk).  The state is stored K-major, so
+o_t = scale * S_t^T q_t; the recurrence written V-major,
+S <- e^g S (I - beta k k^T) + beta v k^T, o = S q, is the same operator.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _native
+
+__all__ = [
+    "chunk_gated_delta_rule",
+    "fused_recurrent_gated_delta_rule",
+    "chunk_workspace_bytes",
+]
+
+CHUNK_SIZE = 64
+_HEAD_SIZES = (64, 128)
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _check_inputs(q, k, v, g, beta, initial_state, cu_seqlens, name):
+    for nm, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise ValueError(f"{name}: {nm} must be a torch.Tensor")
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name}: {nm} must have dtype torch.bfloat16, got {t.dtype}.")
+        if t.dim() != 4:
+            raise ValueError(f"{name}: {nm} must be 4-D [B, T, H, D], got {tuple(t.shape)}.")
+    B, T, Hqk, K = q.shape
+    if tuple(k.shape) != (B, T, Hqk, K):
+        raise ValueError(f"{name}: k must have shape {tuple(q.shape)}, got {tuple(k.shape)}.")
+    if tuple(v.shape[:2]) != (B, T):
+        raise ValueError(f"{name}: v must have shape [B, T, Hv, V] with B, T = {B}, {T}.")
+    Hv, V = v.shape[2], v.shape[3]
+    if Hqk == 0 or Hv % Hqk != 0:
+        raise ValueError(f"{name}: v-heads ({Hv}) must be a multiple of qk-heads ({Hqk}).")
+    if K not in _HEAD_SIZES or V not in _HEAD_SIZES:
+        raise ValueError(f"{name}: head sizes K={K}, V={V} unsupported (each in {_HEAD_SIZES}).")
+    for nm, t in (("g", g), ("beta", beta)):
+        if not isinstance(t, torch.Tensor):
+            raise ValueError(f"{name}: {nm} must be a torch.Tensor")
+        if tuple(t.shape) != (B, T, Hv):
+            raise ValueError(f"{name}: {nm} must have shape {(B, T, Hv)}, got {tuple(t.shape)}.")
+        if not t.is_floating_point():
+            raise ValueError(f"{name}: {nm} must be floating point, got {t.dtype}.")
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError(f"{name}: tensors must be on a ROCm (cuda) device, got {dev}.")
+    for nm, t in (("k", k), ("v", v), ("g", g), ("beta", beta)):
+        if t.device != dev:
+            raise ValueError(f"{name}: {nm} must be on {dev}, got {t.device}.")
+
+    if cu_seqlens is not None:
+        if B != 1:
+            raise ValueError(f"{name}: cu_seqlens requires batch size 1, got {B}.")
+        if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+            raise ValueError(f"{name}: cu_seqlens must be 1-D with at least 2 entries.")
+        if cu_seqlens.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"{name}: cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}.")
+        N = cu_seqlens.numel() - 1
+        if cu_seqlens.device.type == "cpu":
+            c = cu_seqlens.tolist()
+            if c[0] != 0 or c[-1] != T or any(b < a for a, b in zip(c[:-1], c[1:])):
+                raise ValueError(f"{name}: cu_seqlens must rise monotonically from 0 to T={T}.")
+        elif cu_seqlens.device != dev:
+            raise ValueError(f"{name}: cu_seqlens must be on {dev} or the CPU.")
+        cu = cu_seqlens.to(device=dev, dtype=torch.int32, non_blocking=True).contiguous()
+    else:
+        N = B
+        cu = None
+
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (N, Hv, K, V):
+            raise ValueError(f"{name}: initial_state must have shape {(N, Hv, K, V)}, "
+                             f"got {tuple(initial_state.shape)}.")
+        if initial_state.dtype != torch.float32:
+            raise ValueError(f"{name}: initial_state must be torch.float32, got {initial_state.dtype}.")
+        if initial_state.device != dev:
+            raise ValueError(f"{name}: initial_state must be on {dev}.")
+    g = g.to(torch.float32).contiguous()
+    beta = beta.to(torch.float32).contiguous()
+    return (q.contiguous(), k.contiguous(), v.contiguous(), g, beta, cu,
+            (B, T, Hqk, Hv, K, V, N))
+
+
+def chunk_workspace_bytes(B: int, T: int, Hqk: int, Hv: int, K: int, V: int, N: int,
+                          has_cu_seqlens: bool, use_qk_l2norm: bool = False) -> int:
+    """Device scratch bytes ``chunk_gated_delta_rule`` needs (gdn_chunk_workspace_bytes)."""
+    return int(_native.lib().gdn_chunk_workspace_bytes(
+        B, T, Hqk, Hv, K, V, N, int(has_cu_seqlens), int(use_qk_l2norm)))
+
+
+def chunk_gated_delta_rule(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    *,
+    workspace: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    final_state: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Chunked (C = 64) gated-delta-rule prefill on gfx950.
+
+    Semantics of torch_chunk_gated_delta_rule (modeling_qwen3_next.py:374-453)
+    with FLA's argument list.  Returns ``(o, final_state)``; ``final_state``
+    is ``None`` unless ``output_final_state``.  ``workspace`` (uint8, at least
+    ``chunk_workspace_bytes(...)``), ``out`` and ``final_state`` may be passed
+    to avoid allocation; ``final_state`` may be ``initial_state`` itself.
+    With ``use_qk_l2norm_in_kernel`` q and k are L2-normalised (eps 1e-6)
+    and rounded to bf16 before use, as FLA's separate l2norm pass does.
+    """
+    name = "chunk_gated_delta_rule"
+    q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
+        q, k, v, g, beta, initial_state, cu_seqlens, name)
+    if scale is None:
+        scale = K ** -0.5
+    dev = q.device
+    o = torch.empty_like(v) if out is None else out
+    if o.shape != v.shape or o.dtype != torch.bfloat16 or o.device != dev or not o.is_contiguous():
+        raise ValueError(f"{name}: out must be a contiguous bf16 tensor of shape {tuple(v.shape)}.")
+    h0 = initial_state.contiguous() if initial_state is not None else None
+    ht = None
+    if output_final_state:
+        if final_state is None:
+            ht = torch.empty((N, Hv, K, V), dtype=torch.float32, device=dev)
+        else:
+            ht = final_state
+            if (tuple(ht.shape) != (N, Hv, K, V) or ht.dtype != torch.float32
+                    or ht.device != dev or not ht.is_contiguous()):
+                raise ValueError(f"{name}: final_state must be contiguous fp32 {(N, Hv, K, V)}.")
+    nbytes = chunk_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu is not None, use_qk_l2norm_in_kernel)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < nbytes or workspace.device != dev:
+        raise ValueError(f"{name}: workspace must be >= {nbytes} bytes on {dev}.")
+    rc = _native.lib().gdn_chunk_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+        _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
+        B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        _stream_ptr(dev))
+    _native.check(rc, name)
+    return o, ht
+
+
+def fused_recurrent_gated_delta_rule(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    inplace_final_state: bool = True,
+    *,
+    out: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Token-by-token gated delta rule (decode) on gfx950.
+
+    Semantics of torch_recurrent_gated_delta_rule (modeling_qwen3_next.py:
+    456-503).  Each (sequence, v-head) state tile is read from HBM once,
+    advanced through that sequence's tokens and written once.  With
+    ``output_final_state`` and ``inplace_final_state`` (and an
+    ``initial_state``) the final state overwrites ``initial_state`` and that
+    tensor is returned; otherwise a new tensor is returned.
+    """
+    name = "fused_recurrent_gated_delta_rule"
+    q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
+        q, k, v, g, beta, initial_state, cu_seqlens, name)
+    if scale is None:
+        scale = K ** -0.5
+    dev = q.device
+    o = torch.empty_like(v) if out is None else out
+    if o.shape != v.shape or o.dtype != torch.bfloat16 or o.device != dev or not o.is_contiguous():
+        raise ValueError(f"{name}: out must be a contiguous bf16 tensor of shape {tuple(v.shape)}.")
+    h0 = initial_state
+    if h0 is not None and not h0.is_contiguous():
+        if output_final_state and inplace_final_state:
+            raise ValueError(f"{name}: an in-place initial_state must be contiguous.")
+        h0 = h0.contiguous()
+    ht = None
+    if output_final_state:
+        if inplace_final_state and h0 is not None:
+            ht = h0
+        else:
+            ht = torch.empty((N, Hv, K, V), dtype=torch.float32, device=dev)
+    rc = _native.lib().gdn_recurrent_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+        _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
+        B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+        _stream_ptr(dev))
+    _native.check(rc, name)
+    return o, ht

@@ -1,0 +1,261 @@
+"""GDN hot-path benchmark on one MI355X (prints ONE JSON line).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Headline (``value``): config 1, Qwen3-Next GDN chunked prefill (B=1,
+T=8192, 16 qk-heads -> 32 v-heads, K=V=128, bf16 q/k/v, fp32 g/beta/state,
+initial state, output_final_state=True) in tokens/s.  A step is one
+``chunk_gated_delta_rule`` call over the whole 8192-token batch; its HIP
+graph (one capture of the call) is replayed K times between two
+``torch.cuda.synchronize()`` calls and timed with events on the stream the
+kernels run on.  Inputs are resident in HBM before timing starts.
+
+Secondary (``decode``): config 2, batch-256 fused-recurrent decode with the
+fp32 state [256, 32, 128, 128] updated in place, 1000 consecutive steps
+cycling a pool of 10 pre-generated q/k/v/g/beta sets; GB/s over
+1,080,098,816 algorithmic bytes per step.
+
+``cpu_baseline``: the C/OpenMP fp32 oracle (oracle/gdn_cpu.c, a port, not the
+reference: the reference has no GDN code) timed on this host's cores.
+Methodology mirrors the reference's GEMM benchmark
+(benchmark/gemm/bench_amdgpu_gemm.py:36-52: warm up, capture, replay, events).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "GDN prefill tokens/s at Qwen3-Next shape; decode state-update GB/s vs HBM peak"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+C = 64
+
+
+def prefill_flops(T, Hv, K=128, V=128):
+    """Algorithmic flops of the chunked prefill: (6CK + 4CV + 6KV) per token per v-head."""
+    return (6 * C * K + 4 * C * V + 6 * K * V) * T * Hv
+
+
+def decode_bytes(N, Hqk, Hv, K=128, V=128):
+    """State read + write (fp32) plus q, k, v, o (bf16) and g, beta (fp32) per step."""
+    return 2 * N * Hv * K * V * 4 + N * (2 * Hqk * K + 2 * Hv * V) * 2 + N * Hv * 2 * 4
+
+
+def _load_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/traffic.json), if present."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def bench_prefill(dev, steps, warmup):
+    from avelang_amd import chunk_gated_delta_rule, chunk_workspace_bytes
+    from avelang_amd import workloads as W
+
+    wl = W.config("cfg1_prefill_qwen3next", seed=1)
+    d = wl.dims
+    t = wl.torch(dev)
+    B, T, Hqk, Hv, K, V, N = (d[x] for x in ("B", "T", "Hqk", "Hv", "K", "V", "N"))
+    ws = torch.empty(chunk_workspace_bytes(B, T, Hqk, Hv, K, V, N, False), dtype=torch.uint8,
+                     device=dev)
+    o = torch.empty_like(t["v"])
+    ht = torch.empty((N, Hv, K, V), dtype=torch.float32, device=dev)
+
+    def call():
+        chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
+                               initial_state=t["initial_state"], output_final_state=True,
+                               workspace=ws, out=o, final_state=ht)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            call()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    w0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - w0
+    ms = e0.elapsed_time(e1) / steps
+    return dict(ms=ms, wall_ms=wall * 1e3 / steps, T=T, Hv=Hv, K=K, V=V, wl=wl)
+
+
+def bench_decode(dev, nsteps=1000, pool=10):
+    from avelang_amd import fused_recurrent_gated_delta_rule
+    from avelang_amd import workloads as W
+
+    sets = [W.config("cfg2_decode_b256", seed=200 + i) for i in range(pool)]
+    d = sets[0].dims
+    N, Hqk, Hv, K, V = (d[x] for x in ("N", "Hqk", "Hv", "K", "V"))
+    ins = [s.torch(dev) for s in sets]
+    state = ins[0]["initial_state"].clone()
+    outs = [torch.empty_like(x["v"]) for x in ins]
+
+    def step(i):
+        x = ins[i % pool]
+        fused_recurrent_gated_delta_rule(x["q"], x["k"], x["v"], x["g"], x["beta"],
+                                         initial_state=state, output_final_state=True,
+                                         inplace_final_state=True, out=outs[i % pool])
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for i in range(pool):
+            step(i)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(pool):
+            step(i)
+    reps = nsteps // pool
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / (reps * pool)
+    return dict(ms=ms, bytes=decode_bytes(N, Hqk, Hv, K, V), N=N, Hqk=Hqk, Hv=Hv, K=K, V=V,
+                steps=reps * pool)
+
+
+def cpu_prefill(wl, runs=5):
+    from oracle import cpu as oracle
+
+    threads = oracle.default_threads()
+    a = wl.numpy()
+    oracle.run("chunk", **a, threads=threads)          # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        oracle.run("chunk", **a, threads=threads)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return dict(value=wl.dims["T"] / med, unit="tokens/s", cores=threads, kind="port",
+                sample=f"config 1 in full (T={wl.dims['T']}, 32 v-heads), C/OpenMP fp32 "
+                       f"chunked oracle, median of {runs} runs ({med * 1e3:.1f} ms each)")
+
+
+def cpu_decode(runs=3):
+    from avelang_amd import workloads as W
+    from oracle import cpu as oracle
+
+    threads = oracle.default_threads()
+    wl = W.config("cfg2_decode_b256", seed=200)
+    a = wl.numpy()
+    d = wl.dims
+    oracle.run("recurrent", **a, threads=threads)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        oracle.run("recurrent", **a, threads=threads)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    nb = decode_bytes(d["N"], d["Hqk"], d["Hv"], d["K"], d["V"])
+    return dict(value=nb / med / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"one full config-2 decode step (256 x 32 state tiles), median of {runs}")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; the GDN operator shards by "
+              "heads with no communication, so --gpus N>1 is not run here.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+
+    pre = bench_prefill(dev, args.steps, args.warmup)
+    dec = bench_decode(dev, args.decode_steps)
+
+    flops = prefill_flops(pre["T"], pre["Hv"], pre["K"], pre["V"])
+    tflops = flops / (pre["ms"] * 1e-3) / 1e12
+    tokens_s = pre["T"] / (pre["ms"] * 1e-3)
+    dec_gbs = dec["bytes"] / (dec["ms"] * 1e-3) / 1e9
+
+    cpu_pre = cpu_dec = None
+    if not args.no_cpu:
+        cpu_pre = cpu_prefill(pre["wl"])
+        cpu_dec = cpu_decode()
+
+    rec = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded numpy PCG64; BASELINE config distributions)",
+        "config": {"workload": "cfg1 GDN chunked prefill, Qwen3-Next shape", "B": 1, "T": pre["T"],
+                   "qk_heads": 16, "v_heads": pre["Hv"], "K": pre["K"], "V": pre["V"], "chunk": C,
+                   "state": "fp32, initial + final", "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": _load_traffic("prefill"),
+                     "kernel": "gdn_chunk_fwd = chunk_table + chunk_prep + chunk_chain",
+                     "algorithmic_flops_per_launch": flops,
+                     "flops_per_token_per_vhead": 6 * C * pre["K"] + 4 * C * pre["V"] + 6 * pre["K"] * pre["V"]},
+        "cpu_baseline": cpu_pre,
+        "decode": {
+            "workload": "cfg2 fused recurrent decode, 256 seqs x 32 v-heads, state in place",
+            "value": round(dec_gbs, 1), "unit": "GB/s", "ms_per_step": round(dec["ms"], 5),
+            "steps": dec["steps"], "tokens_per_s": round(dec["N"] / (dec["ms"] * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": _load_traffic("decode"),
+                         "kernel": "recurrent_kernel<128,128>",
+                         "algorithmic_bytes_per_launch": dec["bytes"]},
+            "cpu_baseline": cpu_dec,
+        },
+        "host_wall_ms_per_step": round(pre["wall_ms"], 5),
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,108 @@
+/*
+ * gdn.h — C ABI of the MI355X (gfx950) gated-delta-net hot path.
+ *
+ * The reference repository (848267592/avelang) ships no gated-delta-rule
+ * code; its only kernel-library entry point is the Python wrapper
+ * `gemm_pipeline_transposed_b` (python/avelang_kernels/amdgpu_gemm.py:458-494)
+ * launched through a generated C launcher that takes raw device pointers,
+ * scalars and torch's current stream (python/avelang/backends/amdgpu/
+ * driver.py:220-392, stream getter backends/driver.py:24-30).  These entry
+ * points take the place of that launcher for the two GDN operators that
+ * Qwen3-Next calls (transformers modeling_qwen3_next.py:658-683):
+ *   chunk_gated_delta_rule            -> gdn_chunk_fwd
+ *   fused_recurrent_gated_delta_rule  -> gdn_recurrent_fwd
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers; the caller owns every buffer.  Nothing
+ *     here allocates device memory or synchronises; work is enqueued on
+ *     `stream` (a hipStream_t; NULL = the legacy default stream).
+ *   - Layouts (row-major, contiguous):
+ *       q, k   [B, T, Hqk, K]  bf16
+ *       v, o   [B, T, Hv,  V]  bf16
+ *       g, beta[B, T, Hv]      fp32   (g = natural-log decay, applied as exp(g))
+ *       state  [N, Hv, K, V]   fp32   (S stored K-major: o_t = scale * S^T q_t)
+ *     v-head h reads qk-head h / (Hv / Hqk).
+ *   - cu_seqlens (nullable) is an int32 device array [N+1] of packed
+ *     sequence offsets; it requires B == 1.  Without it N == B and every
+ *     batch row is one sequence of length T.
+ *   - Return value: 0 = success; < 0 = argument error (nothing enqueued);
+ *     > 0 = a hipError_t from a launch.  gdn_last_error() gives a
+ *     thread-local message for the last failing call of this thread.
+ *   - Supported head sizes: K in {64, 128}; V in {64, 128}.
+ */
+#ifndef AVELANG_AMD_GDN_H
+#define AVELANG_AMD_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Argument-error codes (negative). */
+#define GDN_OK 0
+#define GDN_ERR_NULL (-1)        /* required pointer is NULL            */
+#define GDN_ERR_SHAPE (-2)       /* unsupported or inconsistent shape   */
+#define GDN_ERR_SEQLENS (-3)     /* cu_seqlens / N inconsistent         */
+#define GDN_ERR_WORKSPACE (-4)   /* workspace NULL or too small         */
+#define GDN_ERR_ALIAS (-5)       /* forbidden buffer aliasing           */
+
+/*
+ * Chunked prefill (chunk = 64 tokens).  Replaces the launcher call an
+ * avelang_kernels `chunk_gated_delta_rule` op would make (convention:
+ * amdgpu_gemm.py:488-493 -> driver.py:324-343); operator semantics as
+ * modeling_qwen3_next.py:374-453.
+ *
+ *   h0  nullable: initial state [N, Hv, K, V]; NULL = zeros.
+ *   ht  nullable: final state   [N, Hv, K, V]; NULL = not written.
+ *       ht may equal h0 (in-place update); any other overlap is an error.
+ *   use_qk_l2norm != 0: q and k are L2-normalised over K (eps 1e-6) and
+ *       rounded to bf16 before use.
+ *   max_tokens_per_seq: host-side upper bound of the longest sequence
+ *       (T when cu_seqlens is NULL); only sizes the launch grid.
+ *   workspace: device scratch of at least gdn_chunk_workspace_bytes(...).
+ */
+int gdn_chunk_fwd(const void* q, const void* k, const void* v,
+                  const float* g, const float* beta,
+                  const float* h0, float* ht, void* o,
+                  const int32_t* cu_seqlens,
+                  int B, int T, int Hqk, int Hv, int K, int V, int N,
+                  float scale, int use_qk_l2norm,
+                  void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Bytes of device workspace gdn_chunk_fwd needs for these sizes
+ * (an upper bound when cu_seqlens is used: T/64 + N chunks). */
+size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
+                                 int N, int has_cu_seqlens, int use_qk_l2norm);
+
+/*
+ * Fused recurrent form (decode: T == 1 per sequence; also multi-token).
+ * Replaces the launcher call of `fused_recurrent_gated_delta_rule`
+ * (semantics modeling_qwen3_next.py:456-503).  The state tile of each
+ * (sequence, v-head) is streamed once from HBM, advanced through that
+ * sequence's tokens in registers, and written once.
+ *
+ *   h0 nullable (zeros); ht nullable (not written); ht == h0 updates the
+ *   state in place (the decode configuration).
+ */
+int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
+                      const float* g, const float* beta,
+                      const float* h0, float* ht, void* o,
+                      const int32_t* cu_seqlens,
+                      int B, int T, int Hqk, int Hv, int K, int V, int N,
+                      float scale, int use_qk_l2norm,
+                      void* stream);
+
+/* Thread-local message describing the last failure (never NULL). */
+const char* gdn_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int gdn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AVELANG_AMD_GDN_H */
