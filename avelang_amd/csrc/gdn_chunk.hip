@@ -179,14 +179,16 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   // stage K and Q rows of the chunk
   uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
   uint16_t* Qs = Ks + 64 * LDK;
-  for (int idx = tid; idx < 64 * (K / 8); idx += 256) {
+  // Padding rows (row >= L) repeat row L-1: their A rows are scaled by
+  // beta = 0 and their P rows / columns are never used, so the values only
+  // need to be finite; the loads stay branch-free.
+#pragma unroll
+  for (int it = 0; it < 64 * (K / 8) / 256; ++it) {
+    const int idx = tid + 256 * it;
     const int row = idx / (K / 8), vec = idx % (K / 8);
-    u16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0}, qv = kv;
-    if (row < L) {
-      const size_t src = ((size_t)(t0 + row) * Hqk + hq) * K + vec * 8;
-      kv = *reinterpret_cast<const u16x8*>(k + src);
-      qv = *reinterpret_cast<const u16x8*>(q + src);
-    }
+    const size_t src = ((size_t)(t0 + min(row, L - 1)) * Hqk + hq) * K + vec * 8;
+    const u16x8 kv = *reinterpret_cast<const u16x8*>(k + src);
+    const u16x8 qv = *reinterpret_cast<const u16x8*>(q + src);
     *reinterpret_cast<u16x8*>(Ks + row * LDK + vec * 8) = kv;
     *reinterpret_cast<u16x8*>(Qs + row * LDK + vec * 8) = qv;
   }
@@ -301,7 +303,7 @@ struct ChainIn {
   u16x8 kf[KB], qf[KB];
   u16x8 tf[2][2];
   u16x8 pf[2];
-  float vv[4];
+  uint16_t vv[4];   // raw bf16: converted when consumed so the prefetch never waits
   f32x4 gg;
   float gl;
 };
@@ -314,13 +316,16 @@ __device__ __forceinline__ void chain_load(ChainIn<K>& in, const uint16_t* __res
                                            int Hv, int V, int vt, int w, int lane) {
   constexpr int KB = K / 32;
   const int r16 = lane % 16, grp = lane / 16;
-  const int arow = 16 * w + r16;
-  const u16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  // Rows past the sequence end (L <= row < 64) read row L-1 instead of
+  // zeros: such rows only meet zero columns of Tb (beta = 0 padding) and
+  // zero rows of vnew, so any finite value is exact, and the loads stay
+  // branch-free (no per-load vmcnt wait).
+  const int arow = min(16 * w + r16, L - 1);
   const size_t qk_off = ((size_t)(t0 + arow) * Hqk + hq) * K + 8 * grp;
 #pragma unroll
   for (int b = 0; b < KB; ++b) {
-    in.kf[b] = arow < L ? *reinterpret_cast<const u16x8*>(k + qk_off + 32 * b) : z8;
-    in.qf[b] = arow < L ? *reinterpret_cast<const u16x8*>(q + qk_off + 32 * b) : z8;
+    in.kf[b] = *reinterpret_cast<const u16x8*>(k + qk_off + 32 * b);
+    in.qf[b] = *reinterpret_cast<const u16x8*>(q + qk_off + 32 * b);
   }
   const size_t base = ((size_t)ci * Hv + h) * 4 + w;
 #pragma unroll
@@ -331,8 +336,8 @@ __device__ __forceinline__ void chain_load(ChainIn<K>& in, const uint16_t* __res
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int row = 16 * w + 4 * grp + r;
-    in.vv[r] = row < L ? bf2f(v[((size_t)(t0 + row) * Hv + h) * V + 16 * vt + r16]) : 0.f;
+    const int row = min(16 * w + 4 * grp + r, L - 1);
+    in.vv[r] = v[((size_t)(t0 + row) * Hv + h) * V + 16 * vt + r16];
   }
   const float* gc = ws.gcum + ((size_t)ci * Hv + h) * 64;
   in.gg = *reinterpret_cast<const f32x4*>(gc + 16 * w + 4 * grp);
@@ -401,20 +406,10 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   publish_state();
   __syncthreads();
 
-  ChainIn<K> cur;
-  if (c_begin < c_end)
-    chain_load<K>(cur, q, k, v, ws, c_begin, s, min(kChunk, e - s), h, hq, Hqk, Hv, V, vt, w,
-                  lane);
-
-  for (int ci = c_begin; ci < c_end; ++ci) {
+  // One chunk step; `cur` holds the chunk's operands, prefetched one step ahead.
+  auto step = [&](const ChainIn<K>& cur, int ci) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
-    ChainIn<K> nxt;
-    if (ci + 1 < c_end) {
-      const int t1 = t0 + kChunk;
-      chain_load<K>(nxt, q, k, v, ws, ci + 1, t1, min(kChunk, e - t1), h, hq, Hqk, Hv, V, vt,
-                    w, lane);
-    }
     // stage this chunk's K rows for the K^T operand of the state update
 #pragma unroll
     for (int b = 0; b < KB; ++b)
@@ -436,7 +431,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         eG[r] = __expf(cur.gg[r]);
-        const float y = cur.vv[r] - eG[r] * X[r];
+        const float y = bf2f(cur.vv[r]) - eG[r] * X[r];
         uint16_t a, b;
         split_bf(y, a, b);
         yh[r] = a;
@@ -482,12 +477,16 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
         const u16x8 vb = *reinterpret_cast<const u16x8*>(&VnT[r16][32 * b + 8 * grp]);
         acc = mfma16(cur.pf[b], vb, acc);
       }
+      // Buffer stores bounded to this chunk's L rows: the hardware drops the
+      // padding rows, so the store needs no branch (a branch here would make
+      // the compiler wait for every outstanding load at the loop head).
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          o + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * w + 4 * grp + r;
-        if (row < L)
-          o[((size_t)(t0 + row) * Hv + h) * V + 16 * vt + r16] =
-              f2bf(scale * eG[r] * QS[r] + acc[r]);
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * eG[r] * QS[r] + acc[r]), orsrc,
+                                              ((row * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
       }
     }
     // S = e^G_L S + K^T U   (U hi+lo)
@@ -516,7 +515,26 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     }
     publish_state();
     __syncthreads();
-    if (ci + 1 < c_end) cur = nxt;
+  };
+  auto load = [&](ChainIn<K>& buf, int ci) {
+    const int t0 = s + (ci - c_begin) * kChunk;
+    chain_load<K>(buf, q, k, v, ws, ci, t0, min(kChunk, e - t0), h, hq, Hqk, Hv, V, vt, w,
+                  lane);
+  };
+
+  // Two operand buffers in ping-pong, so a prefetch never has to complete
+  // before the step that does not use it (no register copy of the prefetch).
+  // The prefetch is unconditional (the last chunk reloads itself): a
+  // conditional load would make the wait-count merge at the join fall back
+  // to waiting for every outstanding load.
+  ChainIn<K> bufA, bufB;
+  if (c_begin < c_end) load(bufA, c_begin);
+  for (int ci = c_begin; ci < c_end; ci += 2) {
+    load(bufB, min(ci + 1, c_end - 1));
+    step(bufA, ci);
+    if (ci + 1 >= c_end) break;
+    load(bufA, min(ci + 2, c_end - 1));
+    step(bufB, ci + 1);
   }
 
   if (ht) {

@@ -17,6 +17,9 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 64;  // tokens per chunk of the prefill path
+// Word 3 of a raw (stride 0) buffer resource on gfx950: out-of-range loads
+// return 0 and out-of-range stores are dropped.
+constexpr int kBufferFlags = 0x00020000;
 constexpr int kWave = 64;   // CDNA wavefront width
 
 // bf16 <-> fp32 on raw 16-bit patterns.
@@ -24,12 +27,9 @@ __device__ __forceinline__ float bf2f(uint16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+// fp32 -> bf16, round to nearest even: one v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // Split x into hi + lo bf16 parts with x ~= hi + lo to ~2^-17 relative.
