@@ -35,7 +35,7 @@ namespace gdn {
 // ---------------------------------------------------------------- layout --
 struct ChunkWs {
   int32_t* off;     // [N+1] first global chunk of each sequence
-  float* gcum;      // [NC][Hv][64] within-chunk cumulative log-decay
+  float* gate;      // [NC][Hv][128]: e^G_i (64), then e^(G_last - G_i) (64)
   u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
   u16x8* pfrag;     // [NC][Hv][4][2][64]
   uint16_t* qn;     // l2-normalised copies (only with use_qk_l2norm)
@@ -173,7 +173,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     }
     Gs[lane] = gv;
     Bs[lane] = bv;
-    ws.gcum[((size_t)ci * Hv + h) * 64 + lane] = gv;
+    const float gl = __shfl(gv, L - 1);
+    float* gate = ws.gate + ((size_t)ci * Hv + h) * 128;
+    gate[lane] = __expf(gv);
+    gate[64 + lane] = __expf(gl - gv);
   }
 
   // stage K and Q rows of the chunk
@@ -297,51 +300,72 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 }
 
 // --------------------------------------------------------- chain (K2) ----
+// Operands of one chunk step for wave w (chunk rows 16w..16w+15), fetched one
+// step ahead in three parts so the vector-memory queue never stalls a wave
+// for long: A (K and Q rows) before the K S products, B (Tb, P fragments)
+// after the first barrier, C (V column slice, gate factors) after the second.
 template <int K>
 struct ChainIn {
   static constexpr int KB = K / 32;
-  u16x8 kf[KB], qf[KB];
-  u16x8 tf[2][2];
-  u16x8 pf[2];
-  uint16_t vv[4];   // raw bf16: converted when consumed so the prefetch never waits
-  f32x4 gg;
-  float gl;
+  u16x8 kf[KB], qf[KB];   // K / Q rows, A operand of K S and Q S
+  u16x8 tf[2][2];         // Tb rows [k-block][hi, lo]
+  u16x8 pf[2];            // P rows [k-block]
+  uint16_t vv[4];         // V[row 4grp+r][16 vt + r16], raw bf16
+  f32x4 eg, dec;          // e^G_row, e^(G_last - G_row) for rows 4grp+r
+  float egl;              // e^G_last
+};
+
+struct ChainCtx {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  ChunkWs ws;
+  int s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane;
 };
 
 template <int K>
-__device__ __forceinline__ void chain_load(ChainIn<K>& in, const uint16_t* __restrict__ q,
-                                           const uint16_t* __restrict__ k,
-                                           const uint16_t* __restrict__ v, const ChunkWs& ws,
-                                           int ci, int t0, int L, int h, int hq, int Hqk,
-                                           int Hv, int V, int vt, int w, int lane) {
-  constexpr int KB = K / 32;
-  const int r16 = lane % 16, grp = lane / 16;
+__device__ __forceinline__ void chain_load_a(ChainIn<K>& in, const ChainCtx& c, int ci) {
+  const int t0 = c.s + (ci - c.c_begin) * kChunk;
+  const int L = min(kChunk, c.e - t0);
+  const int r16 = c.lane % 16, grp = c.lane / 16;
   // Rows past the sequence end (L <= row < 64) read row L-1 instead of
   // zeros: such rows only meet zero columns of Tb (beta = 0 padding) and
   // zero rows of vnew, so any finite value is exact, and the loads stay
   // branch-free (no per-load vmcnt wait).
-  const int arow = min(16 * w + r16, L - 1);
-  const size_t qk_off = ((size_t)(t0 + arow) * Hqk + hq) * K + 8 * grp;
+  const int arow = min(16 * c.w + r16, L - 1);
+  const size_t off = ((size_t)(t0 + arow) * c.Hqk + c.hq) * K + 8 * grp;
 #pragma unroll
-  for (int b = 0; b < KB; ++b) {
-    in.kf[b] = *reinterpret_cast<const u16x8*>(k + qk_off + 32 * b);
-    in.qf[b] = *reinterpret_cast<const u16x8*>(q + qk_off + 32 * b);
+  for (int b = 0; b < ChainIn<K>::KB; ++b) {
+    in.kf[b] = *reinterpret_cast<const u16x8*>(c.k + off + 32 * b);
+    in.qf[b] = *reinterpret_cast<const u16x8*>(c.q + off + 32 * b);
   }
-  const size_t base = ((size_t)ci * Hv + h) * 4 + w;
+}
+
+template <int K>
+__device__ __forceinline__ void chain_load_b(ChainIn<K>& in, const ChainCtx& c, int ci) {
+  const size_t base = ((size_t)ci * c.Hv + c.h) * 4 + c.w;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    in.tf[b][0] = ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + lane];
-    in.tf[b][1] = ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane];
-    in.pf[b] = ws.pfrag[(base * 2 + b) * 64 + lane];
+    in.tf[b][0] = c.ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + c.lane];
+    in.tf[b][1] = c.ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + c.lane];
+    in.pf[b] = c.ws.pfrag[(base * 2 + b) * 64 + c.lane];
   }
+}
+
+template <int K>
+__device__ __forceinline__ void chain_load_c(ChainIn<K>& in, const ChainCtx& c, int ci) {
+  const int t0 = c.s + (ci - c.c_begin) * kChunk;
+  const int L = min(kChunk, c.e - t0);
+  const int r16 = c.lane % 16, grp = c.lane / 16;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int row = min(16 * w + 4 * grp + r, L - 1);
-    in.vv[r] = v[((size_t)(t0 + row) * Hv + h) * V + 16 * vt + r16];
+    const int row = min(16 * c.w + 4 * grp + r, L - 1);
+    in.vv[r] = c.v[((size_t)(t0 + row) * c.Hv + c.h) * c.V + 16 * c.vt + r16];
   }
-  const float* gc = ws.gcum + ((size_t)ci * Hv + h) * 64;
-  in.gg = *reinterpret_cast<const f32x4*>(gc + 16 * w + 4 * grp);
-  in.gl = gc[L - 1];
+  const float* gate = c.ws.gate + ((size_t)ci * c.Hv + c.h) * 128;
+  in.eg = *reinterpret_cast<const f32x4*>(gate + 16 * c.w + 4 * grp);
+  in.dec = *reinterpret_cast<const f32x4*>(gate + 64 + 16 * c.w + 4 * grp);
+  in.egl = gate[L - 1];
 }
 
 template <int K>
@@ -354,6 +378,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   constexpr int RT = K / 64;     // 16-row state tiles per wave
   constexpr int LDS_ = K + 8;    // S^T row stride (bf16)
   constexpr int LDY = 72;        // 64-row operands
+  static_assert(KB % 2 == 0, "K S uses two accumulators per hi/lo part");
   __shared__ __attribute__((aligned(16))) uint16_t SsT[2][16][LDS_];
   __shared__ __attribute__((aligned(16))) uint16_t YsT[2][16][LDY];
   __shared__ __attribute__((aligned(16))) uint16_t UsT[2][16][LDY];
@@ -375,6 +400,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   int s, e;
   seq_bounds(cu, n, T, total, s, e);
   const int c_begin = ws.off[n], c_end = ws.off[n + 1];
+  const ChainCtx ctx{q, k, v, ws, s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane};
 
   // state slice: rows w*16*RT + 16*tt + 4*grp + r, column 16*vt + r16
   const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
@@ -406,32 +432,39 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   publish_state();
   __syncthreads();
 
-  // One chunk step; `cur` holds the chunk's operands, prefetched one step ahead.
-  auto step = [&](const ChainIn<K>& cur, int ci) {
+  // One chunk step on `cur` (chunk ci) while `nxt` is filled for chunk cn.
+  // Every accumulation is split over independent accumulators so no MFMA
+  // chain is more than two deep (a dependent 16x16x32 MFMA costs ~34 cycles).
+  auto step = [&](const ChainIn<K>& cur, ChainIn<K>& nxt, int ci, int cn) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
+    chain_load_a<K>(nxt, ctx, cn);
     // stage this chunk's K rows for the K^T operand of the state update
 #pragma unroll
     for (int b = 0; b < KB; ++b)
       *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = cur.kf[b];
 
-    // X = K S (hi+lo), QS = Q S (hi)
-    f32x4 X = zero4(), QS = zero4();
+    // X = K S (hi + lo), QS = Q S (hi)
+    f32x4 xa = zero4(), xb = zero4(), xc = zero4(), xd = zero4(), qa = zero4(), qb = zero4();
 #pragma unroll
-    for (int b = 0; b < KB; ++b) {
-      const u16x8 sh = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]);
-      const u16x8 sl = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 8 * grp]);
-      X = mfma16(cur.kf[b], sh, X);
-      X = mfma16(cur.kf[b], sl, X);
-      QS = mfma16(cur.qf[b], sh, QS);
+    for (int b = 0; b < KB; b += 2) {
+      const u16x8 sh0 = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]);
+      const u16x8 sl0 = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 8 * grp]);
+      const u16x8 sh1 = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]);
+      const u16x8 sl1 = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 32 + 8 * grp]);
+      xa = mfma16(cur.kf[b], sh0, xa);
+      xb = mfma16(cur.kf[b + 1], sh1, xb);
+      xc = mfma16(cur.kf[b], sl0, xc);
+      xd = mfma16(cur.kf[b + 1], sl1, xd);
+      qa = mfma16(cur.qf[b], sh0, qa);
+      qb = mfma16(cur.qf[b + 1], sh1, qb);
     }
-    float eG[4];
     {
+      const f32x4 X = (xa + xb) + (xc + xd);
       u16x4 yh, yl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        eG[r] = __expf(cur.gg[r]);
-        const float y = bf2f(cur.vv[r]) - eG[r] * X[r];
+        const float y = bf2f(cur.vv[r]) - cur.eg[r] * X[r];
         uint16_t a, b;
         split_bf(y, a, b);
         yh[r] = a;
@@ -441,24 +474,39 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       *reinterpret_cast<u16x4*>(&YsT[1][r16][16 * w + 4 * grp]) = yl;
     }
     __syncthreads();
+    chain_load_b<K>(nxt, ctx, cn);
 
-    // vnew = Tb Y (3-term hi/lo)
-    f32x4 vn = zero4();
+    // K^T fragments of the update, gathered now (off the critical path)
+    u16x8 ka[RT][2];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const u16x8 yh = *reinterpret_cast<const u16x8*>(&YsT[0][r16][32 * b + 8 * grp]);
-      const u16x8 yl = *reinterpret_cast<const u16x8*>(&YsT[1][r16][32 * b + 8 * grp]);
-      vn = mfma16(cur.tf[b][0], yh, vn);
-      vn = mfma16(cur.tf[b][0], yl, vn);
-      vn = mfma16(cur.tf[b][1], yh, vn);
+    for (int tt = 0; tt < RT; ++tt) {
+      const int kd = w * 16 * RT + 16 * tt + r16;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int ii = 0; ii < 8; ++ii) ka[tt][b][ii] = Kl[32 * b + 8 * grp + ii][kd];
+    }
+
+    // vnew = Tb Y (three hi/lo terms, independent accumulators)
+    f32x4 vn;
+    {
+      f32x4 va = zero4(), vb = zero4(), vc = zero4();
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const u16x8 yh = *reinterpret_cast<const u16x8*>(&YsT[0][r16][32 * b + 8 * grp]);
+        const u16x8 yl = *reinterpret_cast<const u16x8*>(&YsT[1][r16][32 * b + 8 * grp]);
+        va = mfma16(cur.tf[b][0], yh, va);
+        vb = mfma16(cur.tf[b][0], yl, vb);
+        vc = mfma16(cur.tf[b][1], yh, vc);
+      }
+      vn = va + (vb + vc);
     }
     {
       u16x4 uh, ul, vb;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float u = __expf(cur.gl - cur.gg[r]) * vn[r];
         uint16_t a, b;
-        split_bf(u, a, b);
+        split_bf(cur.dec[r] * vn[r], a, b);
         uh[r] = a;
         ul[r] = b;
         vb[r] = f2bf(vn[r]);
@@ -468,30 +516,10 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
     }
     __syncthreads();
+    chain_load_c<K>(nxt, ctx, cn);
 
-    // o = scale e^G (Q S) + P vnew
+    // S = e^G_L S + K^T U   (U hi + lo)
     {
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const u16x8 vb = *reinterpret_cast<const u16x8*>(&VnT[r16][32 * b + 8 * grp]);
-        acc = mfma16(cur.pf[b], vb, acc);
-      }
-      // Buffer stores bounded to this chunk's L rows: the hardware drops the
-      // padding rows, so the store needs no branch (a branch here would make
-      // the compiler wait for every outstanding load at the loop head).
-      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-          o + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * grp + r;
-        __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * eG[r] * QS[r] + acc[r]), orsrc,
-                                              ((row * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
-      }
-    }
-    // S = e^G_L S + K^T U   (U hi+lo)
-    {
-      const float egl = __expf(cur.gl);
       u16x8 uh[2], ul[2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
@@ -500,41 +528,52 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       }
 #pragma unroll
       for (int tt = 0; tt < RT; ++tt) {
-        const int kd = w * 16 * RT + 16 * tt + r16;
-        f32x4 acc = Sr[tt] * egl;
+        f32x4 a0 = Sr[tt] * cur.egl, a1 = zero4();
+        a0 = mfma16(ka[tt][0], uh[0], a0);
+        a1 = mfma16(ka[tt][0], ul[0], a1);
+        a0 = mfma16(ka[tt][1], uh[1], a0);
+        a1 = mfma16(ka[tt][1], ul[1], a1);
+        Sr[tt] = a0 + a1;
+      }
+    }
+    // o = scale e^G (Q S) + P vnew
+    {
+      const u16x8 v0 = *reinterpret_cast<const u16x8*>(&VnT[r16][8 * grp]);
+      const u16x8 v1 = *reinterpret_cast<const u16x8*>(&VnT[r16][32 + 8 * grp]);
+      const f32x4 oa = mfma16(cur.pf[0], v0, zero4());
+      const f32x4 ob = mfma16(cur.pf[1], v1, zero4());
+      const f32x4 QS = qa + qb;
+      // Buffer stores bounded to this chunk's L rows: the hardware drops the
+      // padding rows, so the store needs no branch (a branch here would make
+      // the compiler wait for every outstanding load at the loop head).
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          o + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          u16x8 ka;
-#pragma unroll
-          for (int ii = 0; ii < 8; ++ii) ka[ii] = Kl[32 * b + 8 * grp + ii][kd];
-          acc = mfma16(ka, uh[b], acc);
-          acc = mfma16(ka, ul[b], acc);
-        }
-        Sr[tt] = acc;
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * w + 4 * grp + r;
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * cur.eg[r] * QS[r] + (oa[r] + ob[r])),
+                                              orsrc, ((row * Hv + h) * V + 16 * vt + r16) * 2,
+                                              0, 0);
       }
     }
     publish_state();
     __syncthreads();
   };
-  auto load = [&](ChainIn<K>& buf, int ci) {
-    const int t0 = s + (ci - c_begin) * kChunk;
-    chain_load<K>(buf, q, k, v, ws, ci, t0, min(kChunk, e - t0), h, hq, Hqk, Hv, V, vt, w,
-                  lane);
-  };
 
-  // Two operand buffers in ping-pong, so a prefetch never has to complete
-  // before the step that does not use it (no register copy of the prefetch).
-  // The prefetch is unconditional (the last chunk reloads itself): a
-  // conditional load would make the wait-count merge at the join fall back
-  // to waiting for every outstanding load.
+  // Two operand buffers in ping-pong: a prefetch never has to complete before
+  // the step that does not use it.  The prefetch is unconditional (the last
+  // chunk reloads itself): a conditional load would make the wait-count merge
+  // at the join fall back to waiting for every outstanding load.
   ChainIn<K> bufA, bufB;
-  if (c_begin < c_end) load(bufA, c_begin);
+  if (c_begin < c_end) {
+    chain_load_a<K>(bufA, ctx, c_begin);
+    chain_load_b<K>(bufA, ctx, c_begin);
+    chain_load_c<K>(bufA, ctx, c_begin);
+  }
   for (int ci = c_begin; ci < c_end; ci += 2) {
-    load(bufB, min(ci + 1, c_end - 1));
-    step(bufA, ci);
+    step(bufA, bufB, ci, min(ci + 1, c_end - 1));
     if (ci + 1 >= c_end) break;
-    load(bufA, min(ci + 2, c_end - 1));
-    step(bufB, ci + 1);
+    step(bufB, bufA, ci + 1, min(ci + 2, c_end - 1));
   }
 
   if (ht) {
@@ -553,7 +592,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsPlan {
-  size_t off, gcum, tfrag, pfrag, qn, kn, total;
+  size_t off, gate, tfrag, pfrag, qn, kn, total;
   long long ncmax;
 };
 
@@ -564,8 +603,8 @@ static WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int N, bool has_cu, 
   size_t at = 0;
   p.off = at;
   at = align256(at + (size_t)(N + 1) * 4);
-  p.gcum = at;
-  at = align256(at + (size_t)p.ncmax * Hv * 64 * 4);
+  p.gate = at;
+  at = align256(at + (size_t)p.ncmax * Hv * 128 * 4);
   p.tfrag = at;
   at = align256(at + (size_t)p.ncmax * Hv * 4 * 2 * 2 * 64 * 16);
   p.pfrag = at;
@@ -589,7 +628,7 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
                          hipStream_t st) {
   ChunkWs ws;
   ws.off = reinterpret_cast<int32_t*>(wsb + p.off);
-  ws.gcum = reinterpret_cast<float*>(wsb + p.gcum);
+  ws.gate = reinterpret_cast<float*>(wsb + p.gate);
   ws.tfrag = reinterpret_cast<u16x8*>(wsb + p.tfrag);
   ws.pfrag = reinterpret_cast<u16x8*>(wsb + p.pfrag);
   ws.qn = reinterpret_cast<uint16_t*>(wsb + p.qn);
