@@ -674,7 +674,7 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
   int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk, Hv,
                                      K, V, N);
   if (rc) return rc;
-  if (N == 0) return GDN_OK;
+  if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
   const gdn::WsPlan p =
       gdn::plan_ws(B, T, Hqk, Hv, K, N, cu_seqlens != nullptr, use_qk_l2norm != 0);
   if (!workspace || workspace_bytes < p.total)

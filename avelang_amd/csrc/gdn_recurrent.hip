@@ -173,7 +173,7 @@ extern "C" int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
   int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk,
                                      Hv, K, V, N);
   if (rc) return rc;
-  if (N == 0 || Hv == 0) return GDN_OK;
+  if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
   auto* qq = static_cast<const uint16_t*>(q);
   auto* kk = static_cast<const uint16_t*>(k);
   auto* vv = static_cast<const uint16_t*>(v);

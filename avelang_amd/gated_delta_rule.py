@@ -67,6 +67,13 @@ def _check_inputs(q, k, v, g, beta, initial_state, cu_seqlens, name):
             raise ValueError(f"{name}: {nm} must have shape {(B, T, Hv)}, got {tuple(t.shape)}.")
         if not t.is_floating_point():
             raise ValueError(f"{name}: {nm} must be floating point, got {t.dtype}.")
+    if cu_seqlens is not None:
+        if B != 1:
+            raise ValueError(f"{name}: cu_seqlens requires batch size 1, got {B}.")
+        if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+            raise ValueError(f"{name}: cu_seqlens must be 1-D with at least 2 entries.")
+        if cu_seqlens.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"{name}: cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}.")
     dev = q.device
     if dev.type != "cuda":
         raise ValueError(f"{name}: tensors must be on a ROCm (cuda) device, got {dev}.")
@@ -75,12 +82,6 @@ def _check_inputs(q, k, v, g, beta, initial_state, cu_seqlens, name):
             raise ValueError(f"{name}: {nm} must be on {dev}, got {t.device}.")
 
     if cu_seqlens is not None:
-        if B != 1:
-            raise ValueError(f"{name}: cu_seqlens requires batch size 1, got {B}.")
-        if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
-            raise ValueError(f"{name}: cu_seqlens must be 1-D with at least 2 entries.")
-        if cu_seqlens.dtype not in (torch.int32, torch.int64):
-            raise ValueError(f"{name}: cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}.")
         N = cu_seqlens.numel() - 1
         if cu_seqlens.device.type == "cpu":
             c = cu_seqlens.tolist()

@@ -1,0 +1,117 @@
+"""The C ABI library loads without a GPU, exports every entry point that
+include/gdn.h declares, and rejects bad arguments before launching anything
+(negative codes + a thread-local message).  No compute call needs a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from avelang_amd import _native
+    return _native.lib()
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "gdn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    assert _declared() == ["gdn_abi_version", "gdn_chunk_fwd", "gdn_chunk_workspace_bytes",
+                           "gdn_last_error", "gdn_recurrent_fwd"]
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from avelang_amd import _native
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_native.EXPORTS) == set(_declared())
+    assert lib.gdn_abi_version() == 100
+
+
+def _rec(lib, **kw):
+    p = dict(q=1 << 20, k=2 << 20, v=3 << 20, g=4 << 20, beta=5 << 20, h0=None, ht=None,
+             o=6 << 20, cu=None,
+             B=1, T=4, Hqk=2, Hv=4, K=128, V=128, N=1, scale=0.1, l2=0, stream=None)
+    p.update(kw)
+    return lib.gdn_recurrent_fwd(p["q"], p["k"], p["v"], p["g"], p["beta"], p["h0"], p["ht"],
+                                 p["o"], p["cu"], p["B"], p["T"], p["Hqk"], p["Hv"], p["K"],
+                                 p["V"], p["N"], p["scale"], p["l2"], p["stream"])
+
+
+def _chunk(lib, ws=None, wsb=0, **kw):
+    p = dict(q=1 << 20, k=2 << 20, v=3 << 20, g=4 << 20, beta=5 << 20, h0=None, ht=None,
+             o=6 << 20, cu=None,
+             B=1, T=4, Hqk=2, Hv=4, K=128, V=128, N=1, scale=0.1, l2=0, stream=None)
+    p.update(kw)
+    return lib.gdn_chunk_fwd(p["q"], p["k"], p["v"], p["g"], p["beta"], p["h0"], p["ht"],
+                             p["o"], p["cu"], p["B"], p["T"], p["Hqk"], p["Hv"], p["K"],
+                             p["V"], p["N"], p["scale"], p["l2"], ws, wsb, p["stream"])
+
+
+@pytest.mark.parametrize("fn", [_rec, _chunk])
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(Hv=3), -2, "multiple of Hqk"),
+    (dict(K=96), -2, "unsupported head sizes"),
+    (dict(V=32), -2, "unsupported head sizes"),
+    (dict(T=-1), -2, "non-negative"),
+    (dict(N=2), -3, "N must equal B"),
+    (dict(cu=8, B=2, N=2), -3, "B == 1"),
+    (dict(q=None), -1, "non-NULL"),
+    (dict(o=None), -1, "non-NULL"),
+    (dict(h0=7 << 20, ht=(7 << 20) + 64), -5, "must equal h0"),
+    (dict(o=1 << 20), -5, "must not overlap"),
+])
+def test_argument_errors(lib, fn, kw, code, msg):
+    from avelang_amd import _native
+    rc = fn(lib, **kw)
+    assert rc == code
+    assert msg in _native.last_error()
+
+
+def test_chunk_workspace_checked_before_launch(lib):
+    from avelang_amd import _native
+    need = lib.gdn_chunk_workspace_bytes(1, 4, 2, 4, 128, 128, 1, 0, 0)
+    assert need > 0
+    assert _chunk(lib, ws=None, wsb=0) == -4
+    assert "workspace needs" in _native.last_error()
+    assert _chunk(lib, ws=8 << 20, wsb=need - 1) == -4
+
+
+def test_workspace_bytes_grow_with_problem(lib):
+    f = lib.gdn_chunk_workspace_bytes
+    a = f(1, 8192, 16, 32, 128, 128, 1, 0, 0)
+    b = f(1, 16384, 16, 32, 128, 128, 1, 0, 0)
+    c = f(1, 8192, 16, 32, 128, 128, 64, 1, 0)
+    d = f(1, 8192, 16, 32, 128, 128, 1, 0, 1)
+    assert 0 < a < b and c > a and d > a
+    # per (chunk, v-head): 128 gate floats + 16 KiB Tb + 8 KiB P fragments
+    assert a >= 128 * 32 * (512 + 16384 + 8192)
+
+
+def test_empty_problem_is_a_noop(lib):
+    assert _rec(lib, T=0, q=None, k=None, v=None, g=None, beta=None, o=None) == 0
+    assert _chunk(lib, T=0, B=0, N=0, q=None, k=None, v=None, g=None, beta=None, o=None) == 0
+
+
+def test_last_error_is_thread_local(lib):
+    import threading
+    from avelang_amd import _native
+    assert _rec(lib, Hv=3) == -2
+    seen = {}
+
+    def other():
+        assert _rec(lib, K=96) == -2
+        seen["msg"] = _native.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert "K=96" in seen["msg"]
+    assert "multiple of Hqk" in _native.last_error()
