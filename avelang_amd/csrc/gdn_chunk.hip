@@ -110,34 +110,47 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restr
 }
 
 // ---------------------------------------------------------- prep (K1) ----
-constexpr int kLdA = 68;   // fp32 row stride of A / Tm in LDS
+constexpr int kLdA = 68;   // fp32 row stride of A / Tm in LDS (rows 16-byte aligned)
 constexpr int kLdP = 72;   // bf16 row stride of P in LDS
-constexpr int kLdM = 17;
+constexpr int kLdM = 20;   // fp32 row stride of the block-product scratch
 
-// acc[r] += sum_k X[(4*grp + r) * ldx + k] * Y[k * ldy + c]   (16x16x16, fp32)
+// acc[r] += sum_k X[4*grp + r][k] * Y[k][c]: a 16x16x16 fp32 block product
+// (rows of X read as float4; X, Y in LDS).
 __device__ __forceinline__ void blk_mm(float acc[4], const float* X, int ldx, const float* Y,
                                        int ldy, int c, int grp) {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const float y = Y[k * ldy + c];
+  for (int k4 = 0; k4 < 16; k4 += 4) {
+    float y[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] += X[(4 * grp + r) * ldx + k] * y;
+    for (int kk = 0; kk < 4; ++kk) y[kk] = Y[(k4 + kk) * ldy + c];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(X + (4 * grp + r) * ldx + k4);
+      acc[r] += x[0] * y[0];
+      acc[r] += x[1] * y[1];
+      acc[r] += x[2] * y[2];
+      acc[r] += x[3] * y[3];
+    }
   }
 }
 
+// One workgroup per (chunk, v-head).  Wave w owns chunk rows 16w..16w+15.
 template <int K>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ g, const float* __restrict__ beta,
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, float scale,
     ChunkWs ws) {
-  constexpr int LDK = K + 8;
   constexpr int KB = K / 32;
-  constexpr int kPhase1 = 2 * 64 * LDK * 2;
-  constexpr int kPhase2 = 2 * 64 * kLdA * 4 + 64 * kLdP * 2 + 4 * 16 * kLdM * 4;
-  constexpr int kBytes = kPhase1 > kPhase2 ? kPhase1 : kPhase2;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kBytes];
-  __shared__ float Gs[64], Bs[64];
+  __shared__ __attribute__((aligned(16))) float Af[64 * kLdA];
+  __shared__ __attribute__((aligned(16))) float Tm[64 * kLdA];
+  __shared__ __attribute__((aligned(16))) uint16_t Ps[64 * kLdP];
+  // AdT (diagonal blocks of A, transposed) is dead once the diagonal blocks
+  // are inverted; the off-diagonal products then reuse it as Msc.
+  __shared__ __attribute__((aligned(16))) float Scr[4 * 16 * kLdM];
+  float (*AdT)[16][16] = reinterpret_cast<float (*)[16][16]>(Scr);
+  float (*Msc)[16 * kLdM] = reinterpret_cast<float (*)[16 * kLdM]>(Scr);
+  __shared__ __attribute__((aligned(16))) float Bs[64];
 
   const int ci = blockIdx.x;
   const int h = blockIdx.y;
@@ -159,43 +172,45 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
   const int r16 = lane % 16, grp = lane / 16;
 
-  // gates: inclusive scan of g (padding rows contribute 0)
-  if (w == 0) {
-    float gv = 0.f, bv = 0.f;
-    if (lane < L) {
-      gv = g[(size_t)(t0 + lane) * Hv + h];
-      bv = beta[(size_t)(t0 + lane) * Hv + h];
+  // K / Q rows straight into MFMA fragments (A: this wave's rows; B: the
+  // rows of every earlier tile).  Padding rows (row >= L) repeat row L-1:
+  // their A rows are scaled by beta = 0 and their P entries are never used,
+  // so the values only need to be finite, and the loads stay branch-free.
+  auto rowoff = [&](int row) {
+    return ((size_t)(t0 + min(row, L - 1)) * Hqk + hq) * K + 8 * grp;
+  };
+  u16x8 ka[KB], qa[KB], kt[3][KB];
+  {
+    const size_t ro = rowoff(16 * w + r16);
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      ka[b] = *reinterpret_cast<const u16x8*>(k + ro + 32 * b);
+      qa[b] = *reinterpret_cast<const u16x8*>(q + ro + 32 * b);
     }
 #pragma unroll
-    for (int d = 1; d < 64; d *= 2) {
-      const float o = __shfl_up(gv, d);
-      if (lane >= d) gv += o;
+    for (int tc = 0; tc < 3; ++tc) {
+      const size_t rt = rowoff(16 * min(tc, w) + r16);
+#pragma unroll
+      for (int b = 0; b < KB; ++b) kt[tc][b] = *reinterpret_cast<const u16x8*>(k + rt + 32 * b);
     }
-    Gs[lane] = gv;
-    Bs[lane] = bv;
+  }
+  // gates: every wave scans g over the 64 rows itself (padding rows add 0)
+  const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
+  float gv = g[grow], bv = beta[grow];
+  gv = lane < L ? gv : 0.f;
+  bv = lane < L ? bv : 0.f;
+#pragma unroll
+  for (int d = 1; d < 64; d *= 2) {
+    const float o = __shfl_up(gv, d);
+    if (lane >= d) gv += o;
+  }
+  if (w == 0) {
     const float gl = __shfl(gv, L - 1);
     float* gate = ws.gate + ((size_t)ci * Hv + h) * 128;
     gate[lane] = __expf(gv);
     gate[64 + lane] = __expf(gl - gv);
+    Bs[lane] = bv;
   }
-
-  // stage K and Q rows of the chunk
-  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* Qs = Ks + 64 * LDK;
-  // Padding rows (row >= L) repeat row L-1: their A rows are scaled by
-  // beta = 0 and their P rows / columns are never used, so the values only
-  // need to be finite; the loads stay branch-free.
-#pragma unroll
-  for (int it = 0; it < 64 * (K / 8) / 256; ++it) {
-    const int idx = tid + 256 * it;
-    const int row = idx / (K / 8), vec = idx % (K / 8);
-    const size_t src = ((size_t)(t0 + min(row, L - 1)) * Hqk + hq) * K + vec * 8;
-    const u16x8 kv = *reinterpret_cast<const u16x8*>(k + src);
-    const u16x8 qv = *reinterpret_cast<const u16x8*>(q + src);
-    *reinterpret_cast<u16x8*>(Ks + row * LDK + vec * 8) = kv;
-    *reinterpret_cast<u16x8*>(Qs + row * LDK + vec * 8) = qv;
-  }
-  __syncthreads();
 
   // K K^T and Q K^T for row tile w, column tiles <= w
   f32x4 kk[4], qk[4];
@@ -206,49 +221,58 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     if (tc <= w) {
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
-        const u16x8 bk = *reinterpret_cast<const u16x8*>(Ks + (16 * tc + r16) * LDK + 32 * b + 8 * grp);
-        const u16x8 ak = *reinterpret_cast<const u16x8*>(Ks + (16 * w + r16) * LDK + 32 * b + 8 * grp);
-        const u16x8 aq = *reinterpret_cast<const u16x8*>(Qs + (16 * w + r16) * LDK + 32 * b + 8 * grp);
-        kk[tc] = mfma16(ak, bk, kk[tc]);
-        qk[tc] = mfma16(aq, bk, qk[tc]);
+        const u16x8 bk = tc == w ? ka[b] : kt[tc < 3 ? tc : 0][b];
+        kk[tc] = mfma16(ka[b], bk, kk[tc]);
+        qk[tc] = mfma16(qa[b], bk, qk[tc]);
       }
     }
   }
-  __syncthreads();  // K/Q staging area is reused below
 
-  float* Af = reinterpret_cast<float*>(smem);
-  float* Tm = Af + 64 * kLdA;
-  uint16_t* Ps = reinterpret_cast<uint16_t*>(Tm + 64 * kLdA);
-  float* Msc = reinterpret_cast<float*>(Ps + 64 * kLdP);
-
+  // A = strict_lower(beta_i K K^T Gam), P = scale lower_incl(Q K^T Gam)
+  float Gi[4], Bi[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    Gi[r] = __shfl(gv, 16 * w + 4 * grp + r);
+    Bi[r] = __shfl(bv, 16 * w + 4 * grp + r);
+  }
 #pragma unroll
   for (int tc = 0; tc < 4; ++tc) {
     const int j = 16 * tc + r16;
+    const float Gj = __shfl(gv, j);
+    f32x4 av;
+    u16x4 pv;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 16 * w + 4 * grp + r;
-      float a = 0.f, p = 0.f;
-      if (tc <= w && j <= i) {
-        const float gam = __expf(Gs[i] - Gs[j]);
-        p = scale * qk[tc][r] * gam;
-        if (j < i) a = Bs[i] * kk[tc][r] * gam;
-      }
-      if (tc <= w) Af[i * kLdA + j] = a;
-      Ps[i * kLdP + j] = f2bf(p);
+      const float gam = (tc <= w && j <= i) ? __expf(Gi[r] - Gj) : 0.f;
+      av[r] = (j < i) ? Bi[r] * kk[tc][r] * gam : 0.f;
+      pv[r] = f2bf(scale * qk[tc][r] * gam);
+      Ps[i * kLdP + j] = pv[r];
+      if (tc <= w) Af[i * kLdA + j] = av[r];
     }
+    if (tc == w) *reinterpret_cast<f32x4*>(&AdT[w][r16][4 * grp]) = av;
   }
   __syncthreads();
 
-  // (I + A)^-1, blocked by 16: diagonal blocks by forward substitution
+  // (I + A)^-1, blocked by 16.  Diagonal blocks: right-looking elimination,
+  // lane c < 16 owns column c (15 dependent levels, not 120).
   if (lane < 16) {
-    const float* Ab = Af + 16 * w * kLdA + 16 * w;
     float t[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = (i == lane) ? 1.f : 0.f;
+    for (int i = 0; i < 16; ++i) t[i] = (i == lane) ? 1.f : 0.f;
 #pragma unroll
-      for (int j = 0; j < i; ++j) acc -= Ab[i * kLdA + j] * t[j];
-      t[i] = acc;
+    for (int j = 0; j < 15; ++j) {
+      float col[16];
+#pragma unroll
+      for (int i4 = 0; i4 < 16; i4 += 4) {
+        const f32x4 c4 = *reinterpret_cast<const f32x4*>(&AdT[w][j][i4]);
+        col[i4] = c4[0];
+        col[i4 + 1] = c4[1];
+        col[i4 + 2] = c4[2];
+        col[i4 + 3] = c4[3];
+      }
+#pragma unroll
+      for (int i = j + 1; i < 16; ++i) t[i] -= col[i] * t[j];
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) Tm[(16 * w + i) * kLdA + 16 * w + lane] = t[i];
@@ -265,12 +289,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
         blk_mm(acc, Af + 16 * bi * kLdA + 16 * m, kLdA, Tm + 16 * m * kLdA + 16 * bj, kLdA,
                r16, grp);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Msc[(w * 16 + 4 * grp + r) * kLdM + r16] = acc[r];
+      for (int r = 0; r < 4; ++r) Msc[w][(4 * grp + r) * kLdM + r16] = acc[r];
     }
     __syncthreads();
     if (act) {
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      blk_mm(acc, Tm + 16 * bi * kLdA + 16 * bi, kLdA, Msc + w * 16 * kLdM, kLdM, r16, grp);
+      blk_mm(acc, Tm + 16 * bi * kLdA + 16 * bi, kLdA, Msc[w], kLdM, r16, grp);
 #pragma unroll
       for (int r = 0; r < 4; ++r) Tm[(16 * bi + 4 * grp + r) * kLdA + 16 * bj + r16] = -acc[r];
     }
@@ -282,20 +306,25 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int row = 16 * w + r16;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    u16x8 th, tl, pf;
+    const int c0 = 32 * b + 8 * grp;
+    const f32x4 t0v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0]);
+    const f32x4 t1v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0 + 4]);
+    const f32x4 b0v = *reinterpret_cast<const f32x4*>(&Bs[c0]);
+    const f32x4 b1v = *reinterpret_cast<const f32x4*>(&Bs[c0 + 4]);
+    u16x8 th, tl;
 #pragma unroll
     for (int ii = 0; ii < 8; ++ii) {
-      const int col = 32 * b + 8 * grp + ii;
-      const float x = (col <= row) ? Tm[row * kLdA + col] * Bs[col] : 0.f;
+      const float tv = ii < 4 ? t0v[ii] : t1v[ii - 4];
+      const float bb = ii < 4 ? b0v[ii] : b1v[ii - 4];
+      const float x = (c0 + ii <= row) ? tv * bb : 0.f;
       uint16_t xh, xl;
       split_bf(x, xh, xl);
       th[ii] = xh;
       tl[ii] = xl;
-      pf[ii] = Ps[row * kLdP + col];
     }
     ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + lane] = th;
     ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
-    ws.pfrag[(base * 2 + b) * 64 + lane] = pf;
+    ws.pfrag[(base * 2 + b) * 64 + lane] = *reinterpret_cast<const u16x8*>(&Ps[row * kLdP + c0]);
   }
 }
 
