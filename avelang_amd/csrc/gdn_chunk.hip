@@ -333,6 +333,18 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 // step ahead in three parts so the vector-memory queue never stalls a wave
 // for long: A (K and Q rows) before the K S products, B (Tb, P fragments)
 // after the first barrier, C (V column slice, gate factors) after the second.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// (i % 4) of the 4 x 16-bit words read by lanes 4m + i / 4, m = 0..3.  A
+// group reading 4 rows x 16 columns of a row-major tile thus gets the tile's
+// columns: lane i holds column i of the 4 rows.
+__device__ __forceinline__ u16x4 lds_tr16(const uint16_t* p) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (s16x4 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(u16x4, r);
+}
+
 template <int K>
 struct ChainIn {
   static constexpr int KB = K / 32;
@@ -350,34 +362,42 @@ struct ChainCtx {
   const uint16_t* v;
   ChunkWs ws;
   int s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane;
+  // per-lane byte offsets that do not change from chunk to chunk
+  int kq_off;     // row 16w + r16, columns 8grp.. of a K / Q row
+  int v_off;      // row 16w + 4grp, column 16vt + r16 of V
 };
 
+// Operand loads are raw buffer loads on a per-chunk resource covering the
+// chunk's L rows: rows past the sequence end read as zero (hardware bounds
+// check, no branch, no clamp), the base moves by a scalar per chunk and the
+// per-lane offsets are fixed, so a prefetch costs almost no VALU work.
 template <int K>
 __device__ __forceinline__ void chain_load_a(ChainIn<K>& in, const ChainCtx& c, int ci) {
   const int t0 = c.s + (ci - c.c_begin) * kChunk;
   const int L = min(kChunk, c.e - t0);
-  const int r16 = c.lane % 16, grp = c.lane / 16;
-  // Rows past the sequence end (L <= row < 64) read row L-1 instead of
-  // zeros: such rows only meet zero columns of Tb (beta = 0 padding) and
-  // zero rows of vnew, so any finite value is exact, and the loads stay
-  // branch-free (no per-load vmcnt wait).
-  const int arow = min(16 * c.w + r16, L - 1);
-  const size_t off = ((size_t)(t0 + arow) * c.Hqk + c.hq) * K + 8 * grp;
+  const size_t row0 = (size_t)t0 * c.Hqk + c.hq;
+  const int bytes = L * c.Hqk * K * 2;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(c.k + row0 * K), 0, bytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(c.q + row0 * K), 0, bytes, kBufferFlags);
 #pragma unroll
   for (int b = 0; b < ChainIn<K>::KB; ++b) {
-    in.kf[b] = *reinterpret_cast<const u16x8*>(c.k + off + 32 * b);
-    in.qf[b] = *reinterpret_cast<const u16x8*>(c.q + off + 32 * b);
+    in.kf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, c.kq_off + 64 * b, 0, 0));
+    in.qf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, c.kq_off + 64 * b, 0, 0));
   }
 }
 
 template <int K>
 __device__ __forceinline__ void chain_load_b(ChainIn<K>& in, const ChainCtx& c, int ci) {
   const size_t base = ((size_t)ci * c.Hv + c.h) * 4 + c.w;
+  const u16x8* tb = c.ws.tfrag + base * 256;
+  const u16x8* pb = c.ws.pfrag + base * 128;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    in.tf[b][0] = c.ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + c.lane];
-    in.tf[b][1] = c.ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + c.lane];
-    in.pf[b] = c.ws.pfrag[(base * 2 + b) * 64 + c.lane];
+    in.tf[b][0] = tb[(b * 2 + 0) * 64 + c.lane];
+    in.tf[b][1] = tb[(b * 2 + 1) * 64 + c.lane];
+    in.pf[b] = pb[b * 64 + c.lane];
   }
 }
 
@@ -385,13 +405,15 @@ template <int K>
 __device__ __forceinline__ void chain_load_c(ChainIn<K>& in, const ChainCtx& c, int ci) {
   const int t0 = c.s + (ci - c.c_begin) * kChunk;
   const int L = min(kChunk, c.e - t0);
-  const int r16 = c.lane % 16, grp = c.lane / 16;
+  const int rowb = c.Hv * c.V * 2;
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(c.v + ((size_t)t0 * c.Hv + c.h) * c.V + 16 * c.vt), 0,
+      (L - 1) * rowb + 32, kBufferFlags);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = min(16 * c.w + 4 * grp + r, L - 1);
-    in.vv[r] = c.v[((size_t)(t0 + row) * c.Hv + c.h) * c.V + 16 * c.vt + r16];
-  }
+  for (int r = 0; r < 4; ++r)
+    in.vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, c.v_off + r * rowb, 0, 0);
   const float* gate = c.ws.gate + ((size_t)ci * c.Hv + c.h) * 128;
+  const int grp = c.lane / 16;
   in.eg = *reinterpret_cast<const f32x4*>(gate + 16 * c.w + 4 * grp);
   in.dec = *reinterpret_cast<const f32x4*>(gate + 64 + 16 * c.w + 4 * grp);
   in.egl = gate[L - 1];
@@ -429,7 +451,9 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   int s, e;
   seq_bounds(cu, n, T, total, s, e);
   const int c_begin = ws.off[n], c_end = ws.off[n + 1];
-  const ChainCtx ctx{q, k, v, ws, s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane};
+  const ChainCtx ctx{q, k, v, ws, s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane,
+                     ((16 * w + r16) * Hqk * K + 8 * grp) * 2,
+                     ((16 * w + 4 * grp) * Hv * V + r16) * 2};
 
   // state slice: rows w*16*RT + 16*tt + 4*grp + r, column 16*vt + r16
   const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
@@ -473,8 +497,8 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     for (int b = 0; b < KB; ++b)
       *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = cur.kf[b];
 
-    // X = K S (hi + lo), QS = Q S (hi)
-    f32x4 xa = zero4(), xb = zero4(), xc = zero4(), xd = zero4(), qa = zero4(), qb = zero4();
+    // X = K S (hi + lo); the critical path of the step starts here
+    f32x4 xa = zero4(), xb = zero4(), xc = zero4(), xd = zero4();
 #pragma unroll
     for (int b = 0; b < KB; b += 2) {
       const u16x8 sh0 = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]);
@@ -485,8 +509,6 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       xb = mfma16(cur.kf[b + 1], sh1, xb);
       xc = mfma16(cur.kf[b], sl0, xc);
       xd = mfma16(cur.kf[b + 1], sl1, xd);
-      qa = mfma16(cur.qf[b], sh0, qa);
-      qb = mfma16(cur.qf[b + 1], sh1, qb);
     }
     {
       const f32x4 X = (xa + xb) + (xc + xd);
@@ -505,15 +527,28 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     __syncthreads();
     chain_load_b<K>(nxt, ctx, cn);
 
-    // K^T fragments of the update, gathered now (off the critical path)
+    // K^T fragments of the update, gathered now (off the critical path):
+    // element ii of lane (r16, grp) is Kl[32b + 8grp + ii][kd0 + r16], two
+    // transposing reads of 4 rows each
     u16x8 ka[RT][2];
+    const int m4 = r16 >> 2, q4 = r16 & 3;
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
-      const int kd = w * 16 * RT + 16 * tt + r16;
+      const int kd0 = w * 16 * RT + 16 * tt + 4 * q4;
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < 2; ++b) {
+        const u16x4 lo4 = lds_tr16(&Kl[32 * b + 8 * grp + m4][kd0]);
+        const u16x4 hi4 = lds_tr16(&Kl[32 * b + 8 * grp + 4 + m4][kd0]);
+        ka[tt][b] = u16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+      }
+    }
+    // QS = Q S_hi (needed only for o; S is republished in the last phase)
+    f32x4 qa = zero4(), qb = zero4();
 #pragma unroll
-        for (int ii = 0; ii < 8; ++ii) ka[tt][b][ii] = Kl[32 * b + 8 * grp + ii][kd];
+    for (int b = 0; b < KB; b += 2) {
+      qa = mfma16(cur.qf[b], *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]), qa);
+      qb = mfma16(cur.qf[b + 1],
+                  *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]), qb);
     }
 
     // vnew = Tb Y (three hi/lo terms, independent accumulators)
