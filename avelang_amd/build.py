@@ -28,6 +28,9 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the kernels feed every accumulator to
+    # VALU code, and AGPR results would each need a v_accvgpr_read first.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 
