@@ -144,6 +144,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   constexpr int KB = K / 32;
   __shared__ __attribute__((aligned(16))) float Af[64 * kLdA];
   __shared__ __attribute__((aligned(16))) float Tm[64 * kLdA];
+  // The chunk's K rows are staged in Tm's space until K K^T is formed.
+  static_assert(64 * (K + 8) * 2 <= 64 * kLdA * 4, "K staging must fit in Tm");
+  uint16_t (*Ks)[K + 8] = reinterpret_cast<uint16_t (*)[K + 8]>(Tm);
   __shared__ __attribute__((aligned(16))) uint16_t Ps[64 * kLdP];
   // AdT (diagonal blocks of A, transposed) is dead once the diagonal blocks
   // are inverted; the off-diagonal products then reuse it as Msc.
@@ -172,27 +175,22 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
   const int r16 = lane % 16, grp = lane / 16;
 
-  // K / Q rows straight into MFMA fragments (A: this wave's rows; B: the
-  // rows of every earlier tile).  Padding rows (row >= L) repeat row L-1:
-  // their A rows are scaled by beta = 0 and their P entries are never used,
-  // so the values only need to be finite, and the loads stay branch-free.
-  auto rowoff = [&](int row) {
-    return ((size_t)(t0 + min(row, L - 1)) * Hqk + hq) * K + 8 * grp;
-  };
-  u16x8 ka[KB], qa[KB], kt[3][KB];
+  // K / Q rows straight into MFMA fragments (this wave's rows); the K rows
+  // are also staged in LDS, where the other waves read them as B operands.
+  // Padding rows (row >= L) repeat row L-1: their A rows are scaled by
+  // beta = 0 and their P entries are never used, so the values only need to
+  // be finite, and the loads stay branch-free.
+  u16x8 ka[KB], qa[KB];
   {
-    const size_t ro = rowoff(16 * w + r16);
+    const size_t ro = ((size_t)(t0 + min(16 * w + r16, L - 1)) * Hqk + hq) * K + 8 * grp;
 #pragma unroll
     for (int b = 0; b < KB; ++b) {
       ka[b] = *reinterpret_cast<const u16x8*>(k + ro + 32 * b);
       qa[b] = *reinterpret_cast<const u16x8*>(q + ro + 32 * b);
     }
 #pragma unroll
-    for (int tc = 0; tc < 3; ++tc) {
-      const size_t rt = rowoff(16 * min(tc, w) + r16);
-#pragma unroll
-      for (int b = 0; b < KB; ++b) kt[tc][b] = *reinterpret_cast<const u16x8*>(k + rt + 32 * b);
-    }
+    for (int b = 0; b < KB; ++b)
+      *reinterpret_cast<u16x8*>(&Ks[16 * w + r16][32 * b + 8 * grp]) = ka[b];
   }
   // gates: every wave scans g over the 64 rows itself (padding rows add 0)
   const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
@@ -212,6 +210,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     Bs[lane] = bv;
   }
 
+  __syncthreads();
+
   // K K^T and Q K^T for row tile w, column tiles <= w
   f32x4 kk[4], qk[4];
 #pragma unroll
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     if (tc <= w) {
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
-        const u16x8 bk = tc == w ? ka[b] : kt[tc < 3 ? tc : 0][b];
+        const u16x8 bk = *reinterpret_cast<const u16x8*>(&Ks[16 * tc + r16][32 * b + 8 * grp]);
         kk[tc] = mfma16(ka[b], bk, kk[tc]);
         qk[tc] = mfma16(qa[b], bk, qk[tc]);
       }
