@@ -112,27 +112,6 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restr
 // ---------------------------------------------------------- prep (K1) ----
 constexpr int kLdA = 68;   // fp32 row stride of A / Tm in LDS (rows 16-byte aligned)
 constexpr int kLdP = 72;   // bf16 row stride of P in LDS
-constexpr int kLdM = 20;   // fp32 row stride of the block-product scratch
-
-// acc[r] += sum_k X[4*grp + r][k] * Y[k][c]: a 16x16x16 fp32 block product
-// (rows of X read as float4; X, Y in LDS).
-__device__ __forceinline__ void blk_mm(float acc[4], const float* X, int ldx, const float* Y,
-                                       int ldy, int c, int grp) {
-#pragma unroll
-  for (int k4 = 0; k4 < 16; k4 += 4) {
-    float y[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) y[kk] = Y[(k4 + kk) * ldy + c];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(X + (4 * grp + r) * ldx + k4);
-      acc[r] += x[0] * y[0];
-      acc[r] += x[1] * y[1];
-      acc[r] += x[2] * y[2];
-      acc[r] += x[3] * y[3];
-    }
-  }
-}
 
 // One workgroup per (chunk, v-head).  Wave w owns chunk rows 16w..16w+15.
 template <int K>
@@ -148,11 +127,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   static_assert(64 * (K + 8) * 2 <= 64 * kLdA * 4, "K staging must fit in Tm");
   uint16_t (*Ks)[K + 8] = reinterpret_cast<uint16_t (*)[K + 8]>(Tm);
   __shared__ __attribute__((aligned(16))) uint16_t Ps[64 * kLdP];
-  // AdT (diagonal blocks of A, transposed) is dead once the diagonal blocks
-  // are inverted; the off-diagonal products then reuse it as Msc.
-  __shared__ __attribute__((aligned(16))) float Scr[4 * 16 * kLdM];
-  float (*AdT)[16][16] = reinterpret_cast<float (*)[16][16]>(Scr);
-  float (*Msc)[16 * kLdM] = reinterpret_cast<float (*)[16 * kLdM]>(Scr);
+  // diagonal blocks of A, transposed (column j of block w is AdT[w][j])
+  __shared__ __attribute__((aligned(16))) float AdT[4][16][16];
   __shared__ __attribute__((aligned(16))) float Bs[64];
 
   const int ci = blockIdx.x;
@@ -278,25 +254,28 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     for (int i = 0; i < 16; ++i) Tm[(16 * w + i) * kLdA + 16 * w + lane] = t[i];
   }
   __syncthreads();
-  // off-diagonal blocks by distance d: T_ij = -T_ii * sum_{m=j}^{i-1} A_im T_mj
+  // off-diagonal blocks by distance d: T_ij = -T_ii * sum_{m=j}^{i-1} A_im T_mj,
+  // on fp32 MFMA (16x16x4).  In step s of a 16-deep product lane l supplies
+  // k = 4 (l / 16) + s, so its four A values are one float4 of a row, and
+  // the B operand of the second product is the first product's accumulator
+  // itself (its C layout holds exactly rows 4 (l / 16) + s of column l % 16).
 #pragma unroll
   for (int d = 1; d < 4; ++d) {
     const int bi = w + d, bj = w;
-    const bool act = bi < 4;
-    if (act) {
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int m = bj; m < bi; ++m)
-        blk_mm(acc, Af + 16 * bi * kLdA + 16 * m, kLdA, Tm + 16 * m * kLdA + 16 * bj, kLdA,
-               r16, grp);
+    if (bi < 4) {
+      f32x4 acc = zero4();
+      for (int m = bj; m < bi; ++m) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Af[(16 * bi + r16) * kLdA + 16 * m + 4 * grp]);
+        const float* tb = &Tm[(16 * m + 4 * grp) * kLdA + 16 * bj + r16];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Msc[w][(4 * grp + r) * kLdM + r16] = acc[r];
-    }
-    __syncthreads();
-    if (act) {
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      blk_mm(acc, Tm + 16 * bi * kLdA + 16 * bi, kLdA, Msc[w], kLdM, r16, grp);
+        for (int st = 0; st < 4; ++st) acc = mfma4f32(a4[st], tb[st * kLdA], acc);
+      }
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&Tm[(16 * bi + r16) * kLdA + 16 * bi + 4 * grp]);
+      f32x4 res = zero4();
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Tm[(16 * bi + 4 * grp + r) * kLdA + 16 * bj + r16] = -acc[r];
+      for (int st = 0; st < 4; ++st) res = mfma4f32(d4[st], acc[st], res);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tm[(16 * bi + 4 * grp + r) * kLdA + 16 * bj + r16] = -res[r];
     }
     __syncthreads();
   }

@@ -49,6 +49,12 @@ __device__ __forceinline__ f32x4 mfma16(u16x8 a, u16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(a), as_bf(b), c, 0, 0, 0);
 }
 
+// D = A B + C for fp32 16x16x4 (one block): lane l holds A[l % 16][l / 16]
+// and B[l / 16][l % 16]; D has the same layout as the 16x16x32 bf16 form.
+__device__ __forceinline__ f32x4 mfma4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 }  // namespace gdn
