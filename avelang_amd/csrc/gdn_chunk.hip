@@ -111,7 +111,6 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restr
 
 // ---------------------------------------------------------- prep (K1) ----
 constexpr int kLdA = 68;   // fp32 row stride of A / Tm in LDS (rows 16-byte aligned)
-constexpr int kLdP = 72;   // bf16 row stride of P in LDS
 
 // One workgroup per (chunk, v-head).  Wave w owns chunk rows 16w..16w+15.
 template <int K>
@@ -126,10 +125,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   // The chunk's K rows are staged in Tm's space until K K^T is formed.
   static_assert(64 * (K + 8) * 2 <= 64 * kLdA * 4, "K staging must fit in Tm");
   uint16_t (*Ks)[K + 8] = reinterpret_cast<uint16_t (*)[K + 8]>(Tm);
-  __shared__ __attribute__((aligned(16))) uint16_t Ps[64 * kLdP];
   // diagonal blocks of A, transposed (column j of block w is AdT[w][j])
   __shared__ __attribute__((aligned(16))) float AdT[4][16][16];
   __shared__ __attribute__((aligned(16))) float Bs[64];
+  __shared__ __attribute__((aligned(16))) float Gs[64];
 
   const int ci = blockIdx.x;
   const int h = blockIdx.y;
@@ -168,65 +167,79 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     for (int b = 0; b < KB; ++b)
       *reinterpret_cast<u16x8*>(&Ks[16 * w + r16][32 * b + 8 * grp]) = ka[b];
   }
-  // gates: every wave scans g over the 64 rows itself (padding rows add 0)
-  const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
-  float gv = g[grow], bv = beta[grow];
-  gv = lane < L ? gv : 0.f;
-  bv = lane < L ? bv : 0.f;
-#pragma unroll
-  for (int d = 1; d < 64; d *= 2) {
-    const float o = __shfl_up(gv, d);
-    if (lane >= d) gv += o;
-  }
+  // gates: wave 0 scans g over the 64 rows (padding rows add 0) and shares
+  // G and beta through LDS
   if (w == 0) {
+    const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
+    float gv = g[grow], bv = beta[grow];
+    gv = lane < L ? gv : 0.f;
+    bv = lane < L ? bv : 0.f;
+#pragma unroll
+    for (int d = 1; d < 64; d *= 2) {
+      const float o = __shfl_up(gv, d);
+      if (lane >= d) gv += o;
+    }
     const float gl = __shfl(gv, L - 1);
     float* gate = ws.gate + ((size_t)ci * Hv + h) * 128;
     gate[lane] = __expf(gv);
     gate[64 + lane] = __expf(gl - gv);
+    Gs[lane] = gv;
     Bs[lane] = bv;
   }
-
   __syncthreads();
 
-  // K K^T and Q K^T for row tile w, column tiles <= w
-  f32x4 kk[4], qk[4];
+  // Column tiles tc < w are formed transposed, (K K^T)^T and (Q K^T)^T with
+  // the staged K rows as the A operand: each lane then holds 4 consecutive
+  // columns j of one row i = 16w + r16, so A rows are written as float4 and
+  // P goes straight to its fragment slots.  K K^T is symmetric, so the
+  // transposed tile is the same product.  The diagonal tile is also formed
+  // in the normal orientation for the transposed block AdT.
+  //   A = strict_lower(beta_i K K^T Gam), P = scale lower_incl(Q K^T Gam)
+  const int i = 16 * w + r16;
+  const float Gi = Gs[i], Bi = Bs[i];
+  {
+    f32x4 kd = zero4();
+#pragma unroll
+    for (int b = 0; b < KB; ++b) kd = mfma16(ka[b], ka[b], kd);
+    const f32x4 Gr = *reinterpret_cast<const f32x4*>(&Gs[16 * w + 4 * grp]);
+    const f32x4 Br = *reinterpret_cast<const f32x4*>(&Bs[16 * w + 4 * grp]);
+    f32x4 av;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      // row 16w + 4grp + r, column i
+      av[r] = (i < 16 * w + 4 * grp + r) ? Br[r] * kd[r] * __expf(Gr[r] - Gi) : 0.f;
+    }
+    *reinterpret_cast<f32x4*>(&AdT[w][r16][4 * grp]) = av;
+  }
+  const size_t pbase = (((size_t)ci * Hv + h) * 4 + w) * 2;
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int tc = 0; tc < 4; ++tc) {
-    kk[tc] = zero4();
-    qk[tc] = zero4();
+    f32x4 kt = zero4(), pt = zero4();
     if (tc <= w) {
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
-        const u16x8 bk = *reinterpret_cast<const u16x8*>(&Ks[16 * tc + r16][32 * b + 8 * grp]);
-        kk[tc] = mfma16(ka[b], bk, kk[tc]);
-        qk[tc] = mfma16(qa[b], bk, qk[tc]);
+        const u16x8 kr = *reinterpret_cast<const u16x8*>(&Ks[16 * tc + r16][32 * b + 8 * grp]);
+        kt = mfma16(kr, ka[b], kt);
+        pt = mfma16(kr, qa[b], pt);
       }
     }
-  }
-
-  // A = strict_lower(beta_i K K^T Gam), P = scale lower_incl(Q K^T Gam)
-  float Gi[4], Bi[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    Gi[r] = __shfl(gv, 16 * w + 4 * grp + r);
-    Bi[r] = __shfl(bv, 16 * w + 4 * grp + r);
-  }
-#pragma unroll
-  for (int tc = 0; tc < 4; ++tc) {
-    const int j = 16 * tc + r16;
-    const float Gj = __shfl(gv, j);
+    const f32x4 Gj = *reinterpret_cast<const f32x4*>(&Gs[16 * tc + 4 * grp]);
     f32x4 av;
     u16x4 pv;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = 16 * w + 4 * grp + r;
-      const float gam = (tc <= w && j <= i) ? __expf(Gi[r] - Gj) : 0.f;
-      av[r] = (j < i) ? Bi[r] * kk[tc][r] * gam : 0.f;
-      pv[r] = f2bf(scale * qk[tc][r] * gam);
-      Ps[i * kLdP + j] = pv[r];
-      if (tc <= w) Af[i * kLdA + j] = av[r];
+      const int j = 16 * tc + 4 * grp + r;
+      const float gam = (tc <= w && j <= i) ? __expf(Gi - Gj[r]) : 0.f;
+      av[r] = (j < i) ? Bi * kt[r] * gam : 0.f;
+      pv[r] = f2bf(scale * pt[r] * gam);
     }
-    if (tc == w) *reinterpret_cast<f32x4*>(&AdT[w][r16][4 * grp]) = av;
+    if (tc < w) *reinterpret_cast<f32x4*>(&Af[i * kLdA + 16 * tc + 4 * grp]) = av;
+    // P fragment slot: k-block tc/2, fragment lane r16 + 16 (2 (tc%2) + grp/2),
+    // elements 4 (grp%2) .. +3
+    const size_t pf = (pbase + tc / 2) * 64 + r16 + 16 * (2 * (tc % 2) + grp / 2);
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(ws.pfrag + pf) + 4 * (grp % 2)) =
+        __builtin_bit_cast(u32x2, pv);
   }
   __syncthreads();
 
@@ -303,7 +316,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     }
     ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + lane] = th;
     ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
-    ws.pfrag[(base * 2 + b) * 64 + lane] = *reinterpret_cast<const u16x8*>(&Ps[row * kLdP + c0]);
   }
 }
 
