@@ -132,18 +132,27 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 
   const int ci = blockIdx.x;
   const int h = blockIdx.y;
-  const int32_t* off = ws.off;
-  if (ci >= off[N]) return;
-  // sequence owning chunk ci: largest n < N with off[n] <= ci
-  int lo = 0, hi = N;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (off[mid] <= ci) lo = mid; else hi = mid;
+  int n, cfirst;
+  if (cu) {
+    const int32_t* off = ws.off;
+    if (ci >= off[N]) return;
+    // sequence owning chunk ci: largest n < N with off[n] <= ci
+    int lo = 0, hi = N;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (off[mid] <= ci) lo = mid; else hi = mid;
+    }
+    n = lo;
+    cfirst = off[n];
+  } else {
+    // equal-length sequences: the chunk table is arithmetic
+    const int nct = (T + kChunk - 1) / kChunk;
+    n = ci / nct;
+    cfirst = n * nct;
   }
-  const int n = lo;
   int s, e;
   seq_bounds(cu, n, T, total, s, e);
-  const int t0 = s + (ci - off[n]) * kChunk;
+  const int t0 = s + (ci - cfirst) * kChunk;
   const int L = min(kChunk, e - t0);
   const int hq = h / (Hv / Hqk);
 
@@ -441,7 +450,8 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 
   int s, e;
   seq_bounds(cu, n, T, total, s, e);
-  const int c_begin = ws.off[n], c_end = ws.off[n + 1];
+  const int nct = (T + kChunk - 1) / kChunk;
+  const int c_begin = cu ? ws.off[n] : n * nct, c_end = cu ? ws.off[n + 1] : (n + 1) * nct;
   const ChainCtx ctx{q, k, v, ws, s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane,
                      ((16 * w + r16) * Hqk * K + 8 * grp) * 2,
                      ((16 * w + 4 * grp) * Hv * V + r16) * 2};
@@ -697,8 +707,9 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
     q = ws.qn;
     k = ws.kn;
   }
-  hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, st, cu, N, T, total,
-                     (int)p.ncmax, ws.off);
+  if (cu)
+    hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, st, cu, N, T, total,
+                       (int)p.ncmax, ws.off);
   if (p.ncmax > 0)
     hipLaunchKernelGGL((chunk_prep_kernel<K>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0, st, q,
                        k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws);
