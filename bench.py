@@ -193,7 +193,7 @@ def profile_pass(dev, reps=3):
 
     1. one device-to-device copy of exactly 256 MiB (calibrates FETCH_SIZE /
        WRITE_SIZE against known bytes: 256 MiB read, 256 MiB written);
-    2. ``reps`` config-1 prefill calls (chunk_table, chunk_prep, chunk_chain);
+    2. ``reps`` config-1 prefill calls (chunk_prep, chunk_chain);
     3. ``reps`` config-2 decode steps (recurrent_kernel<128,128>).
     """
     from avelang_amd import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule
@@ -274,7 +274,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": _load_traffic("prefill"),
-                     "kernel": "gdn_chunk_fwd = chunk_table + chunk_prep + chunk_chain",
+                     "kernel": "gdn_chunk_fwd = chunk_prep + chunk_chain (+ chunk_table with cu_seqlens)",
                      "algorithmic_flops_per_launch": flops,
                      "flops_per_token_per_vhead": 6 * C * pre["K"] + 4 * C * pre["V"] + 6 * pre["K"] * pre["V"]},
         "cpu_baseline": cpu_pre,
