@@ -22,7 +22,18 @@ EXPORTS = (
     "gdn_recurrent_fwd",
     "gdn_last_error",
     "gdn_abi_version",
+    # include/gdn_layer.h
+    "gdn_gating_fwd",
+    "gdn_l2norm_fwd",
+    "gdn_causal_conv1d_fwd",
+    "gdn_causal_conv1d_update",
+    "gdn_rmsnorm_gated_fwd",
+    "gdn_recurrent_fwd_indexed",
 )
+
+GDN_DTYPE_F32 = 0
+GDN_DTYPE_BF16 = 1
+GDN_DTYPE_F16 = 2
 
 GDN_OK = 0
 GDN_ERR_NULL = -1
@@ -38,6 +49,7 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+_ll = ctypes.c_longlong
 
 
 class NativeLibraryError(RuntimeError):
@@ -80,6 +92,33 @@ def lib():
         h.gdn_last_error.argtypes = []
         h.gdn_abi_version.restype = _i
         h.gdn_abi_version.argtypes = []
+        h.gdn_gating_fwd.restype = _i
+        h.gdn_gating_fwd.argtypes = [
+            _vp, _vp, _vp, _vp, _vp, _vp,     # A_log a b dt_bias g beta
+            _ll, _i, _i, _i, _i,              # rows H a_dtype b_dtype p_dtype
+            _f, _f, _vp,                      # softplus beta, threshold, stream
+        ]
+        h.gdn_l2norm_fwd.restype = _i
+        h.gdn_l2norm_fwd.argtypes = [_vp, _vp, _ll, _i, _f, _i, _vp]
+        h.gdn_causal_conv1d_fwd.restype = _i
+        h.gdn_causal_conv1d_fwd.argtypes = (
+            [_vp] * 7                         # x weight bias seq_idx init final out
+            + [_i] * 4                        # B D T W
+            + [_ll] * 6                       # x strides, out strides
+            + [_i, _i, _i, _vp])              # silu dtype w_dtype stream
+        h.gdn_causal_conv1d_update.restype = _i
+        h.gdn_causal_conv1d_update.argtypes = (
+            [_vp] * 6                         # x conv_state weight bias indices out
+            + [_i] * 6                        # B D L W S num_slots
+            + [_ll] * 6
+            + [_i, _i, _i, _vp])
+        h.gdn_rmsnorm_gated_fwd.restype = _i
+        h.gdn_rmsnorm_gated_fwd.argtypes = [_vp, _vp, _vp, _vp, _ll, _i, _f, _i, _i, _vp]
+        h.gdn_recurrent_fwd_indexed.restype = _i
+        h.gdn_recurrent_fwd_indexed.argtypes = (
+            [_vp] * 10                        # q k v g beta h0 ht o cu_seqlens state_indices
+            + [_i] * 8                        # B T Hqk Hv K V N num_slots
+            + [_f, _i, _vp])
         _lib = h
         return _lib
 

@@ -32,7 +32,8 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     const uint16_t* __restrict__ v, const float* __restrict__ g,
     const float* __restrict__ beta, const float* h0, float* ht,
     uint16_t* __restrict__ o, const int32_t* __restrict__ cu, int T,
-    int total_tokens, int Hqk, int Hv, float scale, int l2norm) {
+    int total_tokens, int Hqk, int Hv, float scale, int l2norm,
+    const int32_t* __restrict__ slots, int num_slots) {
   constexpr int COLG = V / 4;          // float4 column groups per row
   constexpr int ROWG = NT / COLG;      // row groups
   constexpr int RPT = K / ROWG;        // rows per lane
@@ -62,7 +63,14 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     e = s + T;
   }
 
-  const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V;
+  // state slot of sequence n (a pool of slots under continuous batching;
+  // a slot outside the pool marks a padding sequence, left untouched)
+  int slot = n;
+  if (slots) {
+    slot = slots[n];
+    if (slot < 0 || slot >= num_slots) return;
+  }
+  const size_t tile = ((size_t)slot * Hv + h) * (size_t)K * V;
   f32x4 S[RPT];
   if (h0) {
     const f32x4* src = reinterpret_cast<const f32x4*>(h0 + tile);
@@ -159,11 +167,12 @@ static void launch_recurrent(const uint16_t* q, const uint16_t* k, const uint16_
                              const float* g, const float* beta, const float* h0,
                              float* ht, uint16_t* o, const int32_t* cu, int B, int T,
                              int Hqk, int Hv, int N, float scale, int l2norm,
-                             hipStream_t stream) {
+                             const int32_t* slots, int num_slots, hipStream_t stream) {
   const int total_tokens = B * T;
   constexpr int NT = (K * V >= 128 * 128) ? 512 : 256;
   hipLaunchKernelGGL((recurrent_kernel<K, V, NT>), dim3(N * Hv), dim3(NT), 0, stream, q, k, v,
-                     g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm);
+                     g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm, slots,
+                     num_slots);
 }
 
 }  // namespace gdn
@@ -191,7 +200,7 @@ extern "C" int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
 #define GDN_REC(KK, VV)                                                                   \
   if (K == KK && V == VV) {                                                               \
     gdn::launch_recurrent<KK, VV>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, \
-                                  Hv, N, scale, use_qk_l2norm, st);                       \
+                                  Hv, N, scale, use_qk_l2norm, nullptr, N, st);           \
     return gdn_host::check_launch("gdn_recurrent_fwd");                                   \
   }
   GDN_REC(128, 128)
@@ -200,4 +209,46 @@ extern "C" int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
   GDN_REC(64, 128)
 #undef GDN_REC
   return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd: unsupported K/V");
+}
+
+// Continuous batching: sequence n advances state slot state_indices[n] of a
+// [num_slots, Hv, K, V] pool (declared in gdn_layer.h).
+extern "C" int gdn_recurrent_fwd_indexed(const void* q, const void* k, const void* v,
+                                         const float* g, const float* beta, const float* h0,
+                                         float* ht, void* o, const int32_t* cu_seqlens,
+                                         const int32_t* state_indices, int B, int T, int Hqk,
+                                         int Hv, int K, int V, int N, int num_slots,
+                                         float scale, int use_qk_l2norm, void* stream) {
+  int rc = gdn_host::validate_common(q, k, v, g, beta, nullptr, nullptr, o, cu_seqlens, B, T,
+                                     Hqk, Hv, K, V, N);
+  if (rc) return rc;
+  if (num_slots < 0)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_indexed: num_slots must be >= 0");
+  if (N > 0 && !state_indices)
+    return gdn_host::fail(GDN_ERR_NULL, "gdn_recurrent_fwd_indexed: state_indices must be non-NULL");
+  if (ht && h0 && ht != h0) {
+    const size_t sb = (size_t)num_slots * Hv * K * V * sizeof(float);
+    const auto pa = reinterpret_cast<uintptr_t>(h0), pb = reinterpret_cast<uintptr_t>(ht);
+    if (pa < pb + sb && pb < pa + sb)
+      return gdn_host::fail(GDN_ERR_ALIAS, "gdn_recurrent_fwd_indexed: ht must equal h0 exactly or not overlap it");
+  }
+  if (N == 0 || num_slots == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;
+  auto* qq = static_cast<const uint16_t*>(q);
+  auto* kk = static_cast<const uint16_t*>(k);
+  auto* vv = static_cast<const uint16_t*>(v);
+  auto* oo = static_cast<uint16_t*>(o);
+  auto st = static_cast<hipStream_t>(stream);
+#define GDN_RECI(KK, VV)                                                                  \
+  if (K == KK && V == VV) {                                                               \
+    gdn::launch_recurrent<KK, VV>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, \
+                                  Hv, N, scale, use_qk_l2norm, state_indices, num_slots,  \
+                                  st);                                                    \
+    return gdn_host::check_launch("gdn_recurrent_fwd_indexed");                           \
+  }
+  GDN_RECI(128, 128)
+  GDN_RECI(64, 64)
+  GDN_RECI(128, 64)
+  GDN_RECI(64, 128)
+#undef GDN_RECI
+  return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_indexed: unsupported K/V");
 }

@@ -187,6 +187,7 @@ def fused_recurrent_gated_delta_rule(
     cu_seqlens: Optional[torch.Tensor] = None,
     use_qk_l2norm_in_kernel: bool = False,
     inplace_final_state: bool = True,
+    ssm_state_indices: Optional[torch.Tensor] = None,
     *,
     out: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
@@ -198,8 +199,19 @@ def fused_recurrent_gated_delta_rule(
     ``output_final_state`` and ``inplace_final_state`` (and an
     ``initial_state``) the final state overwrites ``initial_state`` and that
     tensor is returned; otherwise a new tensor is returned.
+
+    Continuous batching: with ``ssm_state_indices`` (int32 [N]) the
+    ``initial_state`` is a pool ``[num_slots, Hv, K, V]`` and sequence n
+    reads slot ``ssm_state_indices[n]``; with ``output_final_state`` the
+    slot is updated in place and the pool returned.  A slot outside
+    ``[0, num_slots)`` marks a padding sequence: its state is untouched and
+    its output rows are left unwritten.  Sequences must use distinct slots.
     """
     name = "fused_recurrent_gated_delta_rule"
+    if ssm_state_indices is not None:
+        return _recurrent_indexed(q, k, v, g, beta, scale, initial_state, output_final_state,
+                                  cu_seqlens, use_qk_l2norm_in_kernel, inplace_final_state,
+                                  ssm_state_indices, out, name)
     q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
         q, k, v, g, beta, initial_state, cu_seqlens, name)
     if scale is None:
@@ -224,5 +236,37 @@ def fused_recurrent_gated_delta_rule(
         _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
         B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
         _stream_ptr(dev))
+    _native.check(rc, name)
+    return o, ht
+
+
+def _recurrent_indexed(q, k, v, g, beta, scale, pool, output_final_state, cu_seqlens,
+                       use_qk_l2norm_in_kernel, inplace_final_state, idx, out, name):
+    if pool is None or not isinstance(pool, torch.Tensor) or pool.dim() != 4:
+        raise ValueError(f"{name}: ssm_state_indices requires initial_state as a state pool "
+                         "[num_slots, Hv, K, V].")
+    if output_final_state and not inplace_final_state:
+        raise ValueError(f"{name}: with ssm_state_indices the final state is written in place.")
+    q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
+        q, k, v, g, beta, None, cu_seqlens, name)
+    dev = q.device
+    if (tuple(pool.shape[1:]) != (Hv, K, V) or pool.dtype != torch.float32
+            or pool.device != dev or not pool.is_contiguous()):
+        raise ValueError(f"{name}: the state pool must be a contiguous fp32 tensor "
+                         f"[num_slots, {Hv}, {K}, {V}] on {dev}.")
+    if (not isinstance(idx, torch.Tensor) or tuple(idx.shape) != (N,)
+            or idx.dtype != torch.int32 or idx.device != dev):
+        raise ValueError(f"{name}: ssm_state_indices must be int32 of shape ({N},) on {dev}.")
+    if scale is None:
+        scale = K ** -0.5
+    o = torch.empty_like(v) if out is None else out
+    if o.shape != v.shape or o.dtype != torch.bfloat16 or o.device != dev or not o.is_contiguous():
+        raise ValueError(f"{name}: out must be a contiguous bf16 tensor of shape {tuple(v.shape)}.")
+    ht = pool if output_final_state else None
+    rc = _native.lib().gdn_recurrent_fwd_indexed(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+        pool.data_ptr(), _ptr(ht), o.data_ptr(), _ptr(cu), idx.contiguous().data_ptr(),
+        B, T, Hqk, Hv, K, V, N, pool.shape[0], float(scale),
+        int(bool(use_qk_l2norm_in_kernel)), _stream_ptr(dev))
     _native.check(rc, name)
     return o, ht

@@ -13,6 +13,9 @@ Contents
                  ``oracle/_build/libgdn_oracle.so``; it is the timed CPU
                  baseline ("port") and a second, independent oracle.
 ``build.py``     gcc recipe for ``gdn_cpu.c``.
+``layer_ref.py`` numpy restatement of the layer's neighbours of the core:
+                 gating, causal conv1d (prefill and decode update), gated
+                 RMSNorm, and the recurrence over a pool of state slots.
 
 The reference tree (848267592/avelang) ships no gated-delta-rule code of
 any kind (``python/avelang_kernels/`` holds only ``amdgpu_gemm.py``), so

@@ -16,15 +16,22 @@ def lib():
     return _native.lib()
 
 
-def _declared():
-    text = open(os.path.join(ROOT, "include", "gdn.h")).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(gdn_\w+)\s*\(", text)))
+def _declared(headers=("gdn.h", "gdn_layer.h")):
+    names = set()
+    for h in headers:
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(gdn_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_expected_entry_points():
-    assert _declared() == ["gdn_abi_version", "gdn_chunk_fwd", "gdn_chunk_workspace_bytes",
-                           "gdn_last_error", "gdn_recurrent_fwd"]
+    assert _declared(("gdn.h",)) == ["gdn_abi_version", "gdn_chunk_fwd",
+                                     "gdn_chunk_workspace_bytes", "gdn_last_error",
+                                     "gdn_recurrent_fwd"]
+    assert _declared(("gdn_layer.h",)) == [
+        "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_gating_fwd",
+        "gdn_l2norm_fwd", "gdn_recurrent_fwd_indexed", "gdn_rmsnorm_gated_fwd"]
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -115,3 +122,85 @@ def test_last_error_is_thread_local(lib):
     t.join()
     assert "K=96" in seen["msg"]
     assert "multiple of Hqk" in _native.last_error()
+
+
+# ------------------------------------------------------- layer operators ----
+def _conv(lib, **kw):
+    p = dict(x=1 << 20, w=2 << 20, bias=None, sq=None, init=None, fin=None, out=3 << 20,
+             B=1, D=16, T=8, W=4, xs=(128, 1, 16), os_=(128, 1, 16), silu=1, dt=1, wdt=1)
+    p.update(kw)
+    return lib.gdn_causal_conv1d_fwd(p["x"], p["w"], p["bias"], p["sq"], p["init"], p["fin"],
+                                     p["out"], p["B"], p["D"], p["T"], p["W"], *p["xs"],
+                                     *p["os_"], p["silu"], p["dt"], p["wdt"], None)
+
+
+def _convu(lib, **kw):
+    p = dict(x=1 << 20, st=2 << 20, w=3 << 20, bias=None, idx=None, out=4 << 20,
+             B=2, D=16, L=1, W=4, S=3, slots=2, xs=(16, 1, 16), os_=(16, 1, 16),
+             silu=1, dt=1, wdt=1)
+    p.update(kw)
+    return lib.gdn_causal_conv1d_update(p["x"], p["st"], p["w"], p["bias"], p["idx"],
+                                        p["out"], p["B"], p["D"], p["L"], p["W"], p["S"],
+                                        p["slots"], *p["xs"], *p["os_"], p["silu"], p["dt"],
+                                        p["wdt"], None)
+
+
+def _reci(lib, **kw):
+    p = dict(q=1 << 20, k=2 << 20, v=3 << 20, g=4 << 20, beta=5 << 20, h0=7 << 20, ht=7 << 20,
+             o=6 << 20, cu=None, idx=8 << 20, B=2, T=1, Hqk=2, Hv=4, K=128, V=128, N=2,
+             slots=4)
+    p.update(kw)
+    return lib.gdn_recurrent_fwd_indexed(p["q"], p["k"], p["v"], p["g"], p["beta"], p["h0"],
+                                         p["ht"], p["o"], p["cu"], p["idx"], p["B"], p["T"],
+                                         p["Hqk"], p["Hv"], p["K"], p["V"], p["N"], p["slots"],
+                                         0.1, 0, None)
+
+
+@pytest.mark.parametrize("call,code,msg", [
+    (lambda l: l.gdn_gating_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 8, 0,
+                                1, 1, 0, 1.0, 20.0, None), -2, "H > 0"),
+    (lambda l: l.gdn_gating_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 8, 4,
+                                7, 1, 0, 1.0, 20.0, None), -2, "dtype"),
+    (lambda l: l.gdn_gating_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 8, 4,
+                                1, 1, 0, 0.0, 20.0, None), -2, "softplus beta"),
+    (lambda l: l.gdn_gating_fwd(None, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 8, 4,
+                                1, 1, 0, 1.0, 20.0, None), -1, "non-NULL"),
+    (lambda l: l.gdn_l2norm_fwd(1 << 20, 2 << 20, 8, 96, 1e-6, 1, None), -2, "64, 128 or 256"),
+    (lambda l: l.gdn_l2norm_fwd(None, 2 << 20, 8, 128, 1e-6, 1, None), -1, "non-NULL"),
+    (lambda l: l.gdn_rmsnorm_gated_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 8, 100, 1e-6, 1, 1,
+                                       None), -2, "64, 128 or 256"),
+    (lambda l: l.gdn_rmsnorm_gated_fwd(1 << 20, None, 3 << 20, 4 << 20, 8, 128, 1e-6, 1, 1,
+                                       None), -1, "non-NULL"),
+    (lambda l: _conv(l, W=5), -2, "W must be"),
+    (lambda l: _conv(l, dt=9), -2, "dtype"),
+    (lambda l: _conv(l, sq=5 << 20, init=6 << 20), -2, "cannot be combined"),
+    (lambda l: _conv(l, x=None), -1, "non-NULL"),
+    (lambda l: _conv(l, out=1 << 20), -5, "alias"),
+    (lambda l: _conv(l, xs=(128, -1, 16)), -2, "strides"),
+    (lambda l: _convu(l, S=2), -2, "state length"),
+    (lambda l: _convu(l, S=9), -2, "state length"),
+    (lambda l: _convu(l, L=65), -2, "tokens per row"),
+    (lambda l: _convu(l, slots=1), -2, "num_slots must be >= B"),
+    (lambda l: _convu(l, st=None), -1, "non-NULL"),
+    (lambda l: _reci(l, idx=None), -1, "state_indices"),
+    (lambda l: _reci(l, ht=(7 << 20) + 64), -5, "must equal h0"),
+    (lambda l: _reci(l, slots=-1), -2, "num_slots"),
+    (lambda l: _reci(l, K=96), -2, "unsupported head sizes"),
+])
+def test_layer_argument_errors(lib, call, code, msg):
+    from avelang_amd import _native
+    rc = call(lib)
+    assert rc == code, _native.last_error()
+    assert msg in _native.last_error()
+
+
+def test_layer_empty_problems_launch_nothing(lib):
+    # zero-sized problems return before touching the (fake) pointers or a device
+    assert lib.gdn_gating_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 0, 4,
+                              1, 1, 0, 1.0, 20.0, None) == 0
+    assert lib.gdn_l2norm_fwd(1 << 20, 2 << 20, 0, 128, 1e-6, 1, None) == 0
+    assert lib.gdn_rmsnorm_gated_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 0, 128, 1e-6, 1, 1,
+                                     None) == 0
+    assert _conv(lib, B=0) == 0
+    assert _convu(lib, B=0) == 0
+    assert _reci(lib, N=0, B=0) == 0

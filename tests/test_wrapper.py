@@ -51,3 +51,45 @@ def test_cu_seqlens_checks(op):
     q, k, v, g, beta = _t()
     with pytest.raises(ValueError, match="int32 or int64"):
         op(q, k, v, g, beta, cu_seqlens=torch.tensor([0.0, 8.0]))
+
+
+# ------------------------------------------------------- layer operators ----
+def test_layer_ops_validate_before_launch():
+    from avelang_amd import layer_ops as L
+    x = torch.zeros(2, 16, 8)
+    w = torch.zeros(16, 4)
+    with pytest.raises(ValueError, match="3-D"):
+        L.causal_conv1d_fn(torch.zeros(16, 8), w)
+    with pytest.raises(ValueError, match="kernel width"):
+        L.causal_conv1d_fn(x, torch.zeros(16, 5))
+    with pytest.raises(ValueError, match="activation"):
+        L.causal_conv1d_fn(x, w, activation="relu")
+    with pytest.raises(ValueError, match="ROCm"):
+        L.causal_conv1d_fn(x, w, activation="silu")
+    with pytest.raises(ValueError, match="conv_state length"):
+        L.causal_conv1d_update(torch.zeros(2, 16), torch.zeros(2, 16, 2), w)
+    with pytest.raises(ValueError, match="1 <= L <= 64"):
+        L.causal_conv1d_update(torch.zeros(2, 16, 65), torch.zeros(2, 16, 3), w)
+    with pytest.raises(ValueError, match="same shape"):
+        L.fused_gdn_gating(torch.zeros(4), torch.zeros(3, 4), torch.zeros(3, 5), torch.zeros(4))
+    with pytest.raises(ValueError, match="shape"):
+        L.fused_gdn_gating(torch.zeros(3), torch.zeros(3, 4), torch.zeros(3, 4), torch.zeros(4))
+    with pytest.raises(ValueError, match="64, 128 or 256"):
+        L.l2norm_fwd(torch.zeros(3, 100))
+    with pytest.raises(ValueError, match="match"):
+        L.rms_norm_gated(torch.zeros(3, 128), torch.zeros(3, 64), torch.zeros(128))
+    with pytest.raises(ValueError, match="float32, bfloat16 or float16"):
+        L.rms_norm_gated(torch.zeros(3, 128, dtype=torch.float64),
+                         torch.zeros(3, 128, dtype=torch.float64), torch.zeros(128))
+
+
+def test_state_pool_validation():
+    q, k, v, g, beta = _t(B=2, T=1)
+    with pytest.raises(ValueError, match="state pool"):
+        fused_recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=None,
+                                         ssm_state_indices=torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(ValueError, match="in place"):
+        fused_recurrent_gated_delta_rule(q, k, v, g, beta,
+                                         initial_state=torch.zeros(3, 4, 128, 128),
+                                         output_final_state=True, inplace_final_state=False,
+                                         ssm_state_indices=torch.zeros(2, dtype=torch.int32))
