@@ -88,12 +88,33 @@ __device__ __forceinline__ void stv(void* p, long long i, const float (&v)[Elt<D
   *reinterpret_cast<uint4*>(static_cast<typename E::T*>(p) + i) = raw;
 }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+// x * sigmoid(x) with the hardware exp and a fast divide (~2 ulp in fp32)
+__device__ __forceinline__ float silu_f(float x) { return __fdividef(x, 1.f + __expf(-x)); }
 
-__device__ __forceinline__ float wave_sum(float v) {
+// M consecutive parameters starting at element e0, converted to fp32: 16-byte
+// loads when M fills whole vectors of the parameter type (e0 aligned to
+// them), element loads otherwise.
+template <int M, int WDT>
+__device__ __forceinline__ void ld_params_t(const void* p, long long e0, float (&out)[M]) {
+  constexpr int PER = Elt<WDT>::VEC;
+  if constexpr (M % PER == 0) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+    for (int v = 0; v < M / PER; ++v) {
+      float tmp[PER];
+      ldv<WDT>(p, e0 + v * PER, tmp);
+#pragma unroll
+      for (int k = 0; k < PER; ++k) out[v * PER + k] = tmp[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < M; ++k) out[k] = lde<WDT>(p, e0 + k);
+  }
+}
+template <int M>
+__device__ __forceinline__ void ld_params(const void* p, long long e0, int wdt, float (&out)[M]) {
+  if (wdt == GDN_DTYPE_F32) ld_params_t<M, GDN_DTYPE_F32>(p, e0, out);
+  else if (wdt == GDN_DTYPE_BF16) ld_params_t<M, GDN_DTYPE_BF16>(p, e0, out);
+  else ld_params_t<M, GDN_DTYPE_F16>(p, e0, out);
 }
 
 // -------------------------------------------------------------- gating ----
@@ -115,26 +136,44 @@ __global__ __launch_bounds__(256) void gating_kernel(const void* A_log, const vo
   }
 }
 
+// Row kernels (l2norm, gated norm): a row of D elements is held by D / VEC
+// lanes with one 16-byte access each (LPR lanes per row, 64 / LPR rows per
+// wavefront), the row sum is a xor-shuffle over those lanes.
+template <int D, int DT>
+struct RowShape {
+  static constexpr int VEC = Elt<DT>::VEC;
+  static constexpr int LPR = D / VEC;          // lanes per row (8 .. 64)
+  static constexpr int RPW = 64 / LPR;         // rows per wavefront
+  static constexpr int RPB = 4 * RPW;          // rows per 256-lane block
+  static_assert(LPR >= 1 && LPR <= 64 && 64 % LPR == 0, "row shape");
+};
+
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
 // -------------------------------------------------------------- l2norm ----
-// One wavefront per row of D; each lane holds D/64 consecutive elements.
 template <int D, int DT>
 __global__ __launch_bounds__(256) void l2norm_kernel(const void* x, void* y, long long rows,
                                                      float eps) {
-  constexpr int E = D / 64;
-  const long long row = (long long)blockIdx.x * 4 + threadIdx.x / 64;
-  if (row >= rows) return;
-  const int lane = threadIdx.x % 64;
-  const long long base = row * D + lane * E;
-  float v[E];
+  using RS = RowShape<D, DT>;
+  constexpr int N = RS::VEC;
+  const long long row = (long long)blockIdx.x * RS::RPB + threadIdx.x / RS::LPR;
+  const int part = threadIdx.x % RS::LPR;
+  const bool live = row < rows;
+  const long long base = (live ? row : 0) * D + part * N;
+  float v[N];
+  ldv<DT>(x, base, v);
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    v[e] = lde<DT>(x, base + e);
-    ss += v[e] * v[e];
-  }
-  const float r = rsqrtf(wave_sum(ss) + eps);
+  for (int c = 0; c < N; ++c) ss += v[c] * v[c];
+  const float r = rsqrtf(group_sum<RS::LPR>(ss) + eps);
 #pragma unroll
-  for (int e = 0; e < E; ++e) ste<DT>(y, base + e, v[e] * r);
+  for (int c = 0; c < N; ++c) v[c] *= r;
+  if (live) stv<DT>(y, base, v);
 }
 
 // ---------------------------------------------------------- gated norm ----
@@ -144,27 +183,30 @@ template <int D, int DT>
 __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const void* x, const void* z,
                                                             const void* weight, void* out,
                                                             long long rows, float eps, int wdt) {
-  constexpr int E = D / 64;
-  const long long row = (long long)blockIdx.x * 4 + threadIdx.x / 64;
-  if (row >= rows) return;
-  const int lane = threadIdx.x % 64;
-  const long long base = row * D + lane * E;
-  float v[E];
+  using RS = RowShape<D, DT>;
+  constexpr int N = RS::VEC;
+  const long long row = (long long)blockIdx.x * RS::RPB + threadIdx.x / RS::LPR;
+  const int part = threadIdx.x % RS::LPR;
+  const bool live = row < rows;
+  const long long base = (live ? row : 0) * D + part * N;
+  float v[N], zv[N];
+  ldv<DT>(x, base, v);
+  ldv<DT>(z, base, zv);
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    v[e] = lde<DT>(x, base + e);
-    ss += v[e] * v[e];
-  }
-  const float r = rsqrtf(wave_sum(ss) / D + eps);
+  for (int c = 0; c < N; ++c) ss += v[c] * v[c];
+  const float r = rsqrtf(group_sum<RS::LPR>(ss) / D + eps);
   const bool round_w = wdt == DT;
+  float wv[N];
+  ld_params<N>(weight, part * N, wdt, wv);
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const float nv = round_to<DT>(v[e] * r);
-    float wn = ldp(weight, lane * E + e, wdt) * nv;
+  for (int c = 0; c < N; ++c) {
+    const float nv = round_to<DT>(v[c] * r);
+    float wn = wv[c] * nv;
     if (round_w) wn = round_to<DT>(wn);
-    ste<DT>(out, base + e, wn * silu_f(lde<DT>(z, base + e)));
+    v[c] = wn * silu_f(zv[c]);
   }
+  if (live) stv<DT>(out, base, v);
 }
 
 // ------------------------------------------------------- causal conv1d ----
@@ -188,18 +230,20 @@ struct ConvArgs {
 template <int DT, int W>
 __global__ __launch_bounds__(256) void conv1d_cl_kernel(ConvArgs a, int TT) {
   constexpr int N = Elt<DT>::VEC;
+  constexpr int U = 8;   // time steps whose loads are issued together
   const int d0 = (blockIdx.x * 64 + threadIdx.x) * N;
   const int b = blockIdx.z;
   const int t0 = (blockIdx.y * 4 + threadIdx.y) * TT;
   if (d0 >= a.D || t0 >= a.T) return;
   const int t1 = min(t0 + TT, a.T);
 
-  float w[W][N], bs[N];
+  float wf[N * W], bs[N];
+  ld_params<N * W>(a.weight, (long long)d0 * W, a.wdt, wf);
+  if (a.bias) {
+    ld_params<N>(a.bias, d0, a.wdt, bs);
+  } else {
 #pragma unroll
-  for (int c = 0; c < N; ++c) {
-#pragma unroll
-    for (int j = 0; j < W; ++j) w[j][c] = ldp(a.weight, (long long)(d0 + c) * W + j, a.wdt);
-    bs[c] = a.bias ? ldp(a.bias, d0 + c, a.wdt) : 0.f;
+    for (int c = 0; c < N; ++c) bs[c] = 0.f;
   }
   const long long xb = (long long)b * a.x_sb + d0;
   const long long ob = (long long)b * a.o_sb + d0;
@@ -223,34 +267,43 @@ __global__ __launch_bounds__(256) void conv1d_cl_kernel(ConvArgs a, int TT) {
       sw[j] = sq ? -2147483647 - 1 : 0;
     }
   }
-  for (int t = t0; t < t1; ++t) {
-    float cur[N];
-    ldv<DT>(a.x, xb + t * a.x_st, cur);
-    const int st = sq ? sq[t] : 0;
-    float acc[N];
+  for (int tb = t0; tb < t1; tb += U) {
+    float cur[U][N];
+    int sc[U];
 #pragma unroll
-    for (int c = 0; c < N; ++c) acc[c] = bs[c] + w[W - 1][c] * cur[c];
+    for (int u = 0; u < U; ++u) {
+      const int t = min(tb + u, t1 - 1);   // clamped: steps past t1 are not used
+      ldv<DT>(a.x, xb + t * a.x_st, cur[u]);
+      sc[u] = sq ? sq[t] : 0;
+    }
 #pragma unroll
-    for (int j = 0; j < W - 1; ++j) {
-      if (sw[j] == st) {
+    for (int u = 0; u < U; ++u) {
+      if (tb + u >= t1) break;
+      float acc[N];
 #pragma unroll
-        for (int c = 0; c < N; ++c) acc[c] += w[j][c] * win[j][c];
+      for (int c = 0; c < N; ++c) acc[c] = bs[c] + wf[c * W + W - 1] * cur[u][c];
+#pragma unroll
+      for (int j = 0; j < W - 1; ++j) {
+        if (sw[j] == sc[u]) {
+#pragma unroll
+          for (int c = 0; c < N; ++c) acc[c] += wf[c * W + j] * win[j][c];
+        }
       }
+      if (a.silu) {
+#pragma unroll
+        for (int c = 0; c < N; ++c) acc[c] = silu_f(acc[c]);
+      }
+      stv<DT>(a.out, ob + (tb + u) * a.o_st, acc);
+#pragma unroll
+      for (int j = 0; j + 1 < W - 1; ++j) {
+#pragma unroll
+        for (int c = 0; c < N; ++c) win[j][c] = win[j + 1][c];
+        sw[j] = sw[j + 1];
+      }
+#pragma unroll
+      for (int c = 0; c < N; ++c) win[W - 2][c] = cur[u][c];
+      sw[W - 2] = sc[u];
     }
-    if (a.silu) {
-#pragma unroll
-      for (int c = 0; c < N; ++c) acc[c] = silu_f(acc[c]);
-    }
-    stv<DT>(a.out, ob + t * a.o_st, acc);
-#pragma unroll
-    for (int j = 0; j + 1 < W - 1; ++j) {
-#pragma unroll
-      for (int c = 0; c < N; ++c) win[j][c] = win[j + 1][c];
-      sw[j] = sw[j + 1];
-    }
-#pragma unroll
-    for (int c = 0; c < N; ++c) win[W - 2][c] = cur[c];
-    sw[W - 2] = st;
   }
   // the tile that ends the row leaves the last W-1 inputs in its window
   if (a.final_states && t1 == a.T) {
@@ -408,6 +461,89 @@ __global__ __launch_bounds__(256) void conv1d_update_kernel(
     if (i < S) ste<DT>(state, sb + i, ns[i]);
 }
 
+// Channel-contiguous inputs (x_sd == o_sd == 1): lane = VEC consecutive
+// channels; their S state inputs are VEC * S consecutive elements (S 16-byte
+// loads), the inputs of one token one 16-byte load.  The last S inputs are
+// kept in registers while the L new tokens stream through.
+template <int DT, int W, int S>
+__device__ __forceinline__ void conv_update_row(const void* x, void* state, void* out,
+                                                long long sb, long long xr, long long orow,
+                                                int L, long long x_st, long long o_st,
+                                                const float (&wf)[Elt<DT>::VEC * W],
+                                                const float (&bs)[Elt<DT>::VEC], int silu) {
+  constexpr int N = Elt<DT>::VEC;
+  float raw[N * S];
+#pragma unroll
+  for (int v = 0; v < S; ++v) {
+    float tmp[N];
+    ldv<DT>(state, sb + v * N, tmp);
+#pragma unroll
+    for (int k = 0; k < N; ++k) raw[v * N + k] = tmp[k];
+  }
+  float hist[S][N];   // hist[i][c]: the i-th oldest kept input of channel c
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+#pragma unroll
+    for (int c = 0; c < N; ++c) hist[i][c] = raw[c * S + i];
+  }
+  for (int t = 0; t < L; ++t) {
+    float cur[N];
+    ldv<DT>(x, xr + t * x_st, cur);
+    float acc[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+      float v = bs[c] + wf[c * W + W - 1] * cur[c];
+#pragma unroll
+      for (int j = 0; j < W - 1; ++j) v += wf[c * W + j] * hist[S - (W - 1) + j][c];
+      acc[c] = silu ? silu_f(v) : v;
+    }
+    stv<DT>(out, orow + t * o_st, acc);
+#pragma unroll
+    for (int i = 0; i + 1 < S; ++i) {
+#pragma unroll
+      for (int c = 0; c < N; ++c) hist[i][c] = hist[i + 1][c];
+    }
+#pragma unroll
+    for (int c = 0; c < N; ++c) hist[S - 1][c] = cur[c];
+  }
+#pragma unroll
+  for (int v = 0; v < S; ++v) {
+    float tmp[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) tmp[k] = hist[(v * N + k) % S][(v * N + k) / S];
+    stv<DT>(state, sb + v * N, tmp);
+  }
+}
+
+// One batch row per lane (RB rows would share one load of the lane's
+// weights, but 4 rows per lane leave too few lanes at decode sizes).
+template <int DT, int W, int S>
+__global__ __launch_bounds__(256) void conv1d_update_vec_kernel(
+    const void* x, void* state, const void* weight, const void* bias, const int32_t* idx,
+    void* out, int B, int D, int L, int num_slots, long long x_sb, long long x_st,
+    long long o_sb, long long o_st, int silu, int wdt) {
+  constexpr int N = Elt<DT>::VEC;
+  constexpr int RB = 1;
+  const int d0 = (blockIdx.x * 256 + threadIdx.x) * N;
+  if (d0 >= D) return;
+  float wf[N * W], bs[N];
+  ld_params<N * W>(weight, (long long)d0 * W, wdt, wf);
+  if (bias) {
+    ld_params<N>(bias, d0, wdt, bs);
+  } else {
+#pragma unroll
+    for (int c = 0; c < N; ++c) bs[c] = 0.f;
+  }
+  const int b1 = min(B, (int)(blockIdx.y + 1) * RB);
+  for (int b = blockIdx.y * RB; b < b1; ++b) {
+    const int slot = idx ? idx[b] : b;
+    if (slot < 0 || slot >= num_slots) continue;
+    conv_update_row<DT, W, S>(x, state, out, ((long long)slot * D + d0) * S,
+                              (long long)b * x_sb + d0, (long long)b * o_sb + d0, L, x_st, o_st,
+                              wf, bs, silu);
+  }
+}
+
 }  // namespace gdn
 
 // ------------------------------------------------------------- host ----
@@ -451,13 +587,16 @@ extern "C" int gdn_l2norm_fwd(const void* x, void* y, long long rows, int D, flo
   if (!dtype_ok(dtype)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_l2norm_fwd: unsupported dtype code");
   if (rows == 0) return GDN_OK;
   if (!x || !y) return gdn_host::fail(GDN_ERR_NULL, "gdn_l2norm_fwd: x and y must be non-NULL");
-  if (rows > (1LL << 40)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_l2norm_fwd: too many rows");
-  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (rows > (1LL << 36)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_l2norm_fwd: too many rows");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_l2norm_fwd: x and y must be 16-byte aligned");
   auto st = static_cast<hipStream_t>(stream);
-#define GDN_L2(DD, TT)                                                                           \
-  if (D == DD && dtype == TT) {                                                                  \
-    hipLaunchKernelGGL((gdn::l2norm_kernel<DD, TT>), grid, dim3(256), 0, st, x, y, rows, eps);   \
-    return gdn_host::check_launch("gdn_l2norm_fwd");                                             \
+#define GDN_L2(DD, TT)                                                                         \
+  if (D == DD && dtype == TT) {                                                                \
+    constexpr int RPB = gdn::RowShape<DD, TT>::RPB;                                            \
+    hipLaunchKernelGGL((gdn::l2norm_kernel<DD, TT>), dim3((unsigned)((rows + RPB - 1) / RPB)), \
+                       dim3(256), 0, st, x, y, rows, eps);                                     \
+    return gdn_host::check_launch("gdn_l2norm_fwd");                                           \
   }
   GDN_L2(64, GDN_DTYPE_F32) GDN_L2(64, GDN_DTYPE_BF16) GDN_L2(64, GDN_DTYPE_F16)
   GDN_L2(128, GDN_DTYPE_F32) GDN_L2(128, GDN_DTYPE_BF16) GDN_L2(128, GDN_DTYPE_F16)
@@ -477,14 +616,18 @@ extern "C" int gdn_rmsnorm_gated_fwd(const void* x, const void* z, const void* w
   if (rows == 0) return GDN_OK;
   if (!x || !z || !weight || !out)
     return gdn_host::fail(GDN_ERR_NULL, "gdn_rmsnorm_gated_fwd: x, z, weight and out must be non-NULL");
-  if (rows > (1LL << 40)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_rmsnorm_gated_fwd: too many rows");
-  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (rows > (1LL << 36)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_rmsnorm_gated_fwd: too many rows");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(z) |
+       reinterpret_cast<uintptr_t>(out)) % 16)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_rmsnorm_gated_fwd: x, z and out must be 16-byte aligned");
   auto st = static_cast<hipStream_t>(stream);
-#define GDN_RN(DD, TT)                                                                      \
-  if (D == DD && dtype == TT) {                                                             \
-    hipLaunchKernelGGL((gdn::rmsnorm_gated_kernel<DD, TT>), grid, dim3(256), 0, st, x, z,   \
-                       weight, out, rows, eps, w_dtype);                                    \
-    return gdn_host::check_launch("gdn_rmsnorm_gated_fwd");                                 \
+#define GDN_RN(DD, TT)                                                                         \
+  if (D == DD && dtype == TT) {                                                                \
+    constexpr int RPB = gdn::RowShape<DD, TT>::RPB;                                            \
+    hipLaunchKernelGGL((gdn::rmsnorm_gated_kernel<DD, TT>),                                    \
+                       dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st, x, z,       \
+                       weight, out, rows, eps, w_dtype);                                       \
+    return gdn_host::check_launch("gdn_rmsnorm_gated_fwd");                                    \
   }
   GDN_RN(64, GDN_DTYPE_F32) GDN_RN(64, GDN_DTYPE_BF16) GDN_RN(64, GDN_DTYPE_F16)
   GDN_RN(128, GDN_DTYPE_F32) GDN_RN(128, GDN_DTYPE_BF16) GDN_RN(128, GDN_DTYPE_F16)
@@ -500,6 +643,8 @@ int launch_conv(const gdn::ConvArgs& a, hipStream_t st) {
   const int N = vec_of(DT);
   const bool vec_aligned_x = (reinterpret_cast<uintptr_t>(a.x) % 16) == 0;
   const bool vec_aligned_o = (reinterpret_cast<uintptr_t>(a.out) % 16) == 0;
+  const bool vec_aligned_w = ((reinterpret_cast<uintptr_t>(a.weight) |
+                               reinterpret_cast<uintptr_t>(a.bias)) % 16) == 0;
   if (a.T == 0) {
     if (a.final_states) {
       const long long n = (long long)a.B * a.D * (W - 1);
@@ -509,8 +654,8 @@ int launch_conv(const gdn::ConvArgs& a, hipStream_t st) {
     return gdn_host::check_launch("gdn_causal_conv1d_fwd");
   }
   if (a.x_sd == 1 && a.o_sd == 1 && a.D % N == 0 && a.x_sb % N == 0 && a.x_st % N == 0 &&
-      a.o_sb % N == 0 && a.o_st % N == 0 && vec_aligned_x && vec_aligned_o) {
-    const int TT = 32;
+      a.o_sb % N == 0 && a.o_st % N == 0 && vec_aligned_x && vec_aligned_o && vec_aligned_w) {
+    const int TT = 16;
     const dim3 grid((unsigned)((a.D / N + 63) / 64), (unsigned)((a.T + 4 * TT - 1) / (4 * TT)),
                     (unsigned)a.B);
     hipLaunchKernelGGL((gdn::conv1d_cl_kernel<DT, W>), grid, dim3(64, 4), 0, st, a, TT);
@@ -589,8 +734,31 @@ extern "C" int gdn_causal_conv1d_update(const void* x, void* conv_state, const v
     return gdn_host::fail(GDN_ERR_NULL, "gdn_causal_conv1d_update: x, conv_state, weight and out must be non-NULL");
   if (B > 65535 || D > (1 << 24))
     return gdn_host::fail(GDN_ERR_SHAPE, "gdn_causal_conv1d_update: problem too large");
-  const dim3 grid((unsigned)((D + 255) / 256), (unsigned)B);
   auto st = static_cast<hipStream_t>(stream);
+  const int N = vec_of(dtype);
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                          reinterpret_cast<uintptr_t>(conv_state) |
+                          reinterpret_cast<uintptr_t>(weight) |
+                          reinterpret_cast<uintptr_t>(bias);
+  // the token stride only matters for L > 1
+  const bool st_ok = L == 1 || (x_st % N == 0 && o_st % N == 0);
+  if (x_sd == 1 && o_sd == 1 && D % N == 0 && x_sb % N == 0 && o_sb % N == 0 && st_ok &&
+      align % 16 == 0 && (S == W - 1 || S == W)) {
+    const dim3 vgrid((unsigned)((D / N + 255) / 256), (unsigned)B);
+#define GDN_CUV(TT, WW, SS)                                                                    \
+    if (dtype == TT && W == WW && S == SS) {                                                   \
+      hipLaunchKernelGGL((gdn::conv1d_update_vec_kernel<TT, WW, SS>), vgrid, dim3(256), 0, st, \
+                         x, conv_state, weight, bias, conv_state_indices, out, B, D, L,        \
+                         num_slots, x_sb, x_st, o_sb, o_st, silu, w_dtype);                    \
+      return gdn_host::check_launch("gdn_causal_conv1d_update");                               \
+    }
+#define GDN_CUV_W(TT) \
+    GDN_CUV(TT, 2, 1) GDN_CUV(TT, 2, 2) GDN_CUV(TT, 3, 2) GDN_CUV(TT, 3, 3) GDN_CUV(TT, 4, 3) GDN_CUV(TT, 4, 4)
+    GDN_CUV_W(GDN_DTYPE_F32) GDN_CUV_W(GDN_DTYPE_BF16) GDN_CUV_W(GDN_DTYPE_F16)
+#undef GDN_CUV_W
+#undef GDN_CUV
+  }
+  const dim3 grid((unsigned)((D + 255) / 256), (unsigned)B);
 #define GDN_CU(TT)                                                                              \
   if (dtype == TT) {                                                                            \
     hipLaunchKernelGGL((gdn::conv1d_update_kernel<TT>), grid, dim3(256), 0, st, x, conv_state,  \

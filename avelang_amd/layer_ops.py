@@ -65,6 +65,12 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (the row kernels move 16 bytes per lane)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _silu_flag(activation: Optional[str], name: str) -> int:
     if activation is None:
         return 0
@@ -133,10 +139,12 @@ def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6,
     dt = _dt(x, name, "x")
     dev = x.device
     _on(dev, name, out=out)
-    x = x.contiguous()
+    x = _aligned(x)
     y = torch.empty_like(x) if out is None else out
-    if y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous():
-        raise ValueError(f"{name}: out must be a contiguous {x.dtype} tensor of shape {tuple(x.shape)}.")
+    if (y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous()
+            or y.data_ptr() % 16):
+        raise ValueError(f"{name}: out must be a contiguous, 16-byte aligned {x.dtype} tensor "
+                         f"of shape {tuple(x.shape)}.")
     rc = _native.lib().gdn_l2norm_fwd(x.data_ptr(), y.data_ptr(), x.numel() // D, D,
                                       float(eps), dt, _stream(dev))
     _native.check(rc, name)
@@ -296,7 +304,7 @@ def rms_norm_gated(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor,
     dt, wdt = _dt(x, name, "x"), _dt(weight, name, "weight")
     dev = x.device
     _on(dev, name, z=z, weight=weight)
-    x, z, weight = x.contiguous(), z.contiguous(), weight.contiguous()
+    x, z, weight = _aligned(x), _aligned(z), weight.contiguous()
     out = torch.empty_like(x)
     rc = _native.lib().gdn_rmsnorm_gated_fwd(x.data_ptr(), z.data_ptr(), weight.data_ptr(),
                                              out.data_ptr(), x.numel() // D, D, float(eps), dt,

@@ -15,6 +15,11 @@ fp32 state [256, 32, 128, 128] updated in place, 1000 consecutive steps
 cycling a pool of 10 pre-generated q/k/v/g/beta sets; GB/s over
 1,080,098,816 algorithmic bytes per step.
 
+``layer_ops``: the layer's neighbours of the core (causal conv1d prefill and
+decode update, gating, l2norm, gated RMSNorm, decode over a state-slot pool)
+at the Qwen3-Next layer shape, each as GB/s over its algorithmic bytes per
+launch (20 launches in one HIP graph, median of 5 replays).
+
 ``cpu_baseline``: the C/OpenMP fp32 oracle (oracle/gdn_cpu.c, a port, not the
 reference: the reference has no GDN code) timed on this host's cores.
 Methodology mirrors the reference's GEMM benchmark
@@ -151,6 +156,85 @@ def bench_decode(dev, nsteps=1000, pool=10):
                 steps=reps * pool)
 
 
+def _time_graph(dev, fn, launches=20, reps=5):
+    """Median per-launch ms of ``fn`` captured ``launches`` times in one HIP graph."""
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(launches):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    times = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1) / launches)
+    return float(np.median(times))
+
+
+def bench_layer_ops(dev):
+    """The layer's neighbours of the core at the Qwen3-Next layer shape
+    (T = 8192, conv_dim = 2 * 16 * 128 + 32 * 128 = 8192; decode batch 256),
+    each against HBM bandwidth with its algorithmic bytes per launch."""
+    from avelang_amd import fused_recurrent_gated_delta_rule, layer_ops as L
+    from avelang_amd import workloads as W
+
+    g = torch.Generator(device=dev).manual_seed(7)
+
+    def rnd(*shape, dtype=torch.bfloat16):
+        return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32).to(dtype)
+
+    T, D, Hqk, Hv, K = 8192, 8192, 16, 32, 128
+    Bd, S, Wk = 256, 3, 4
+    res = {}
+
+    def add(name, fn, nbytes, shape):
+        ms = _time_graph(dev, fn)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"shape": shape, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                     "bytes_per_launch": int(nbytes), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+    x = rnd(1, T, D).transpose(1, 2)                       # the layer's channel-last memory
+    w = rnd(D, Wk)
+    add("causal_conv1d_fn", lambda: L.causal_conv1d_fn(x, w, None, activation="silu"),
+        2 * 2 * D * T, f"x [1, {D}, {T}] bf16 channel-last, W={Wk}, SiLU")
+    xd = rnd(Bd, D)
+    cs = rnd(Bd, D, S)
+    add("causal_conv1d_update", lambda: L.causal_conv1d_update(xd, cs, w, None, activation="silu"),
+        2 * 2 * Bd * D + 2 * 2 * Bd * D * S, f"x [{Bd}, {D}] bf16, state [{Bd}, {D}, {S}] in place")
+    a, b = rnd(1, T, Hv), rnd(1, T, Hv)
+    A_log, dt_bias = torch.zeros(Hv, device=dev), torch.zeros(Hv, device=dev)
+    add("fused_gdn_gating", lambda: L.fused_gdn_gating(A_log, a, b, dt_bias),
+        T * Hv * (2 + 2 + 4 + 4), f"a, b [1, {T}, {Hv}] bf16 -> g, beta fp32")
+    qk = rnd(1, T, Hqk, K)
+    add("l2norm_fwd", lambda: L.l2norm_fwd(qk), 2 * 2 * T * Hqk * K, f"[1, {T}, {Hqk}, {K}] bf16")
+    o, z = rnd(1, T, Hv, K), rnd(1, T, Hv, K)
+    nw = torch.ones(K, device=dev, dtype=torch.bfloat16)
+    add("rms_norm_gated", lambda: L.rms_norm_gated(o, z, nw), 3 * 2 * T * Hv * K,
+        f"o, z [1, {T}, {Hv}, {K}] bf16")
+    dl = W.config("cfg2_decode_b256", seed=300).torch(dev)
+    pool = 0.01 * torch.randn((2 * Bd, Hv, K, K), generator=g, device=dev)
+    idx = torch.randperm(2 * Bd, generator=g, device=dev)[:Bd].to(torch.int32)
+    out = torch.empty_like(dl["v"])
+    add("fused_recurrent_state_pool",
+        lambda: fused_recurrent_gated_delta_rule(dl["q"], dl["k"], dl["v"], dl["g"], dl["beta"],
+                                                 initial_state=pool, output_final_state=True,
+                                                 ssm_state_indices=idx, out=out),
+        decode_bytes(Bd, Hqk, Hv), f"{Bd} sequences over a {2 * Bd}-slot fp32 state pool")
+    return res
+
+
 def cpu_prefill(wl, runs=5):
     from oracle import cpu as oracle
 
@@ -227,6 +311,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-layer-ops", action="store_true",
+                    help="skip the layer-operator measurements")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run the fixed untimed launch sequence used for rocprofv3 --pmc runs")
     args = ap.parse_args()
@@ -244,6 +330,7 @@ def main():
 
     pre = bench_prefill(dev, args.steps, args.warmup)
     dec = bench_decode(dev, args.decode_steps)
+    layer = None if args.no_layer_ops else bench_layer_ops(dev)
 
     flops = prefill_flops(pre["T"], pre["Hv"], pre["K"], pre["V"])
     tflops = flops / (pre["ms"] * 1e-3) / 1e12
@@ -289,6 +376,7 @@ def main():
                          "algorithmic_bytes_per_launch": dec["bytes"]},
             "cpu_baseline": cpu_dec,
         },
+        "layer_ops": layer,
         "host_wall_ms_per_step": round(pre["wall_ms"], 5),
     }
     print(json.dumps(rec), flush=True)
