@@ -655,7 +655,7 @@ int launch_conv(const gdn::ConvArgs& a, hipStream_t st) {
   }
   if (a.x_sd == 1 && a.o_sd == 1 && a.D % N == 0 && a.x_sb % N == 0 && a.x_st % N == 0 &&
       a.o_sb % N == 0 && a.o_st % N == 0 && vec_aligned_x && vec_aligned_o && vec_aligned_w) {
-    const int TT = 16;
+    const int TT = 64;   // halo re-reads (W-1 rows per tile) miss L2: keep tiles long
     const dim3 grid((unsigned)((a.D / N + 63) / 64), (unsigned)((a.T + 4 * TT - 1) / (4 * TT)),
                     (unsigned)a.B);
     hipLaunchKernelGGL((gdn::conv1d_cl_kernel<DT, W>), grid, dim3(64, 4), 0, st, a, TT);

@@ -278,7 +278,8 @@ def profile_pass(dev, reps=3):
     1. one device-to-device copy of exactly 256 MiB (calibrates FETCH_SIZE /
        WRITE_SIZE against known bytes: 256 MiB read, 256 MiB written);
     2. ``reps`` config-1 prefill calls (chunk_prep, chunk_chain);
-    3. ``reps`` config-2 decode steps (recurrent_kernel<128,128>).
+    3. ``reps`` config-2 decode steps (recurrent_kernel<128,128>);
+    4. ``reps`` calls of each layer operator at the Qwen3-Next layer shape.
     """
     from avelang_amd import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule
     from avelang_amd import workloads as W
@@ -300,6 +301,25 @@ def profile_pass(dev, reps=3):
         fused_recurrent_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"],
                                          initial_state=d["initial_state"],
                                          output_final_state=True, inplace_final_state=True)
+    torch.cuda.synchronize(dev)
+    from avelang_amd import layer_ops as L
+    T, D, Hqk, Hv, K = 8192, 8192, 16, 32, 128
+    x = torch.randn(1, T, D, device=dev).to(torch.bfloat16).transpose(1, 2)
+    w = torch.randn(D, 4, device=dev).to(torch.bfloat16)
+    xd = torch.randn(256, D, device=dev).to(torch.bfloat16)
+    cs = torch.randn(256, D, 3, device=dev).to(torch.bfloat16)
+    a = torch.randn(1, T, Hv, device=dev).to(torch.bfloat16)
+    qk = torch.randn(1, T, Hqk, K, device=dev).to(torch.bfloat16)
+    o = torch.randn(1, T, Hv, K, device=dev).to(torch.bfloat16)
+    nw = torch.ones(K, device=dev, dtype=torch.bfloat16)
+    zeros = torch.zeros(Hv, device=dev)
+    torch.cuda.synchronize(dev)
+    for _ in range(reps):
+        L.causal_conv1d_fn(x, w, None, activation="silu")
+        L.causal_conv1d_update(xd, cs, w, None, activation="silu")
+        L.fused_gdn_gating(zeros, a, a, zeros)
+        L.l2norm_fwd(qk)
+        L.rms_norm_gated(o, o, nw)
     torch.cuda.synchronize(dev)
     print("profile pass done", flush=True)
 
