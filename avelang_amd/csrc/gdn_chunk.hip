@@ -38,8 +38,8 @@ struct ChunkWs {
   float* gate;      // [NC][Hv][128]: e^G_i (64), then e^(G_last - G_i) (64)
   u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
   u16x8* pfrag;     // [NC][Hv][4][2][64]
-  uint16_t* qn;     // l2-normalised copies (only with use_qk_l2norm)
-  uint16_t* kn;
+  uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] (use_qk_l2norm only),
+  uint16_t* kn;     // written by the prep kernel, read by the chain
 };
 
 __device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int total,
@@ -51,31 +51,6 @@ __device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int 
     s = n * T;
     e = s + T;
   }
-}
-
-// ------------------------------------------------------------- l2norm ----
-// y = bf16(x * rsqrt(sum x^2 + 1e-6)) per row of K; one wavefront per row.
-template <int K>
-__global__ __launch_bounds__(256) void l2norm_rows_kernel(const uint16_t* __restrict__ x,
-                                                          uint16_t* __restrict__ y,
-                                                          long long rows) {
-  constexpr int PER = K / 64;
-  const long long row = (long long)blockIdx.x * 4 + threadIdx.x / 64;
-  if (row >= rows) return;
-  const int lane = threadIdx.x % 64;
-  const uint16_t* xr = x + row * K + lane * PER;
-  float vals[PER];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    vals[i] = bf2f(xr[i]);
-    ss += vals[i] * vals[i];
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off /= 2) ss += __shfl_xor(ss, off);
-  const float inv = rsqrtf(ss + 1e-6f);
-#pragma unroll
-  for (int i = 0; i < PER; ++i) y[row * K + lane * PER + i] = f2bf(vals[i] * inv);
 }
 
 // -------------------------------------------------------- chunk table ----
@@ -112,13 +87,23 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restr
 // ---------------------------------------------------------- prep (K1) ----
 constexpr int kLdA = 68;   // fp32 row stride of A / Tm in LDS (rows 16-byte aligned)
 
+// Rows of MFMA fragments scaled by r and rounded back to bf16.
+template <int KB>
+__device__ __forceinline__ void scale_frags(u16x8 (&f)[KB], float r) {
+#pragma unroll
+  for (int b = 0; b < KB; ++b) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[b][i] = f2bf(bf2f(f[b][i]) * r);
+  }
+}
+
 // One workgroup per (chunk, v-head).  Wave w owns chunk rows 16w..16w+15.
 template <int K>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ g, const float* __restrict__ beta,
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, float scale,
-    ChunkWs ws) {
+    int l2norm, ChunkWs ws) {
   constexpr int KB = K / 32;
   __shared__ __attribute__((aligned(16))) float Af[64 * kLdA];
   __shared__ __attribute__((aligned(16))) float Tm[64 * kLdA];
@@ -171,6 +156,37 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     for (int b = 0; b < KB; ++b) {
       ka[b] = *reinterpret_cast<const u16x8*>(k + ro + 32 * b);
       qa[b] = *reinterpret_cast<const u16x8*>(q + ro + 32 * b);
+    }
+    if (l2norm) {
+      // use_qk_l2norm: a row's K values sit in the 4 lanes r16 + 16 grp; the
+      // normalised rows are rounded to bf16 (as a separate l2norm pass would
+      // store them), and the first v-head of each qk-head group stores them
+      // for the chain
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float xk = bf2f(ka[b][i]), xq = bf2f(qa[b][i]);
+          sk += xk * xk;
+          sq += xq * xq;
+        }
+      }
+      sk += __shfl_xor(sk, 16);
+      sk += __shfl_xor(sk, 32);
+      sq += __shfl_xor(sq, 16);
+      sq += __shfl_xor(sq, 32);
+      const float rk = rsqrtf(sk + 1e-6f), rq = rsqrtf(sq + 1e-6f);
+      scale_frags<KB>(ka, rk);
+      scale_frags<KB>(qa, rq);
+      if (h % (Hv / Hqk) == 0 && 16 * w + r16 < L) {
+        const size_t wo = ((size_t)(t0 + 16 * w + r16) * Hqk + hq) * K + 8 * grp;
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+          *reinterpret_cast<u16x8*>(ws.kn + wo + 32 * b) = ka[b];
+          *reinterpret_cast<u16x8*>(ws.qn + wo + 32 * b) = qa[b];
+        }
+      }
     }
 #pragma unroll
     for (int b = 0; b < KB; ++b)
@@ -493,10 +509,12 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
     chain_load_a<K>(nxt, ctx, cn);
+    const u16x8* kf = cur.kf;
+    const u16x8* qf = cur.qf;
     // stage this chunk's K rows for the K^T operand of the state update
 #pragma unroll
     for (int b = 0; b < KB; ++b)
-      *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = cur.kf[b];
+      *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = kf[b];
 
     // X = K S (hi + lo); the critical path of the step starts here
     f32x4 xa = zero4(), xb = zero4(), xc = zero4(), xd = zero4();
@@ -506,10 +524,10 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       const u16x8 sl0 = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 8 * grp]);
       const u16x8 sh1 = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]);
       const u16x8 sl1 = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 32 + 8 * grp]);
-      xa = mfma16(cur.kf[b], sh0, xa);
-      xb = mfma16(cur.kf[b + 1], sh1, xb);
-      xc = mfma16(cur.kf[b], sl0, xc);
-      xd = mfma16(cur.kf[b + 1], sl1, xd);
+      xa = mfma16(kf[b], sh0, xa);
+      xb = mfma16(kf[b + 1], sh1, xb);
+      xc = mfma16(kf[b], sl0, xc);
+      xd = mfma16(kf[b + 1], sl1, xd);
     }
     {
       const f32x4 X = (xa + xb) + (xc + xd);
@@ -547,8 +565,8 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     f32x4 qa = zero4(), qb = zero4();
 #pragma unroll
     for (int b = 0; b < KB; b += 2) {
-      qa = mfma16(cur.qf[b], *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]), qa);
-      qb = mfma16(cur.qf[b + 1],
+      qa = mfma16(qf[b], *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]), qa);
+      qb = mfma16(qf[b + 1],
                   *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]), qb);
     }
 
@@ -699,22 +717,16 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
   ws.qn = reinterpret_cast<uint16_t*>(wsb + p.qn);
   ws.kn = reinterpret_cast<uint16_t*>(wsb + p.kn);
   const int total = B * T;
-  if (l2) {
-    const long long rows = (long long)total * Hqk;
-    const unsigned blocks = (unsigned)((rows + 3) / 4);
-    hipLaunchKernelGGL((l2norm_rows_kernel<K>), dim3(blocks), dim3(256), 0, st, q, ws.qn, rows);
-    hipLaunchKernelGGL((l2norm_rows_kernel<K>), dim3(blocks), dim3(256), 0, st, k, ws.kn, rows);
-    q = ws.qn;
-    k = ws.kn;
-  }
   if (cu)
     hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, st, cu, N, T, total,
                        (int)p.ncmax, ws.off);
   if (p.ncmax > 0)
     hipLaunchKernelGGL((chunk_prep_kernel<K>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0, st, q,
-                       k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws);
-  hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, q, k,
-                     v, h0, ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+                       k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
+  // with use_qk_l2norm the chain reads the rows the prep kernel normalised
+  hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st,
+                     l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V,
+                     scale, ws);
 }
 
 }  // namespace gdn

@@ -66,7 +66,7 @@ def _load_traffic(name):
         return None
 
 
-def bench_prefill(dev, steps, warmup):
+def bench_prefill(dev, steps, warmup, l2norm=False):
     from avelang_amd import chunk_gated_delta_rule, chunk_workspace_bytes
     from avelang_amd import workloads as W
 
@@ -74,15 +74,16 @@ def bench_prefill(dev, steps, warmup):
     d = wl.dims
     t = wl.torch(dev)
     B, T, Hqk, Hv, K, V, N = (d[x] for x in ("B", "T", "Hqk", "Hv", "K", "V", "N"))
-    ws = torch.empty(chunk_workspace_bytes(B, T, Hqk, Hv, K, V, N, False), dtype=torch.uint8,
-                     device=dev)
+    ws = torch.empty(chunk_workspace_bytes(B, T, Hqk, Hv, K, V, N, False, l2norm),
+                     dtype=torch.uint8, device=dev)
     o = torch.empty_like(t["v"])
     ht = torch.empty((N, Hv, K, V), dtype=torch.float32, device=dev)
 
     def call():
         chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
                                initial_state=t["initial_state"], output_final_state=True,
-                               workspace=ws, out=o, final_state=ht)
+                               workspace=ws, out=o, final_state=ht,
+                               use_qk_l2norm_in_kernel=l2norm)
 
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))
@@ -351,6 +352,7 @@ def main():
     pre = bench_prefill(dev, args.steps, args.warmup)
     dec = bench_decode(dev, args.decode_steps)
     layer = None if args.no_layer_ops else bench_layer_ops(dev)
+    pre_l2 = bench_prefill(dev, max(args.steps // 2, 1), args.warmup, l2norm=True)
 
     flops = prefill_flops(pre["T"], pre["Hv"], pre["K"], pre["V"])
     tflops = flops / (pre["ms"] * 1e-3) / 1e12
@@ -396,6 +398,10 @@ def main():
                          "algorithmic_bytes_per_launch": dec["bytes"]},
             "cpu_baseline": cpu_dec,
         },
+        "prefill_qk_l2norm_in_kernel": {
+            "workload": "cfg1 as the layer calls it: use_qk_l2norm_in_kernel=True (q, k normalised inside)",
+            "value": round(pre_l2["T"] / (pre_l2["ms"] * 1e-3), 1), "unit": "tokens/s",
+            "ms_per_step": round(pre_l2["ms"], 5)},
         "layer_ops": layer,
         "host_wall_ms_per_step": round(pre["wall_ms"], 5),
     }
