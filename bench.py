@@ -113,6 +113,39 @@ def bench_prefill(dev, steps, warmup, l2norm=False):
     return dict(ms=ms, wall_ms=wall * 1e3 / steps, T=T, Hv=Hv, K=K, V=V, wl=wl)
 
 
+def bench_prefill_config(dev, name, reps=3):
+    """One eager call per repetition of another prefill config (median ms)."""
+    from avelang_amd import chunk_gated_delta_rule
+    from avelang_amd import workloads as W
+
+    wl = W.config(name, seed=1)
+    t = wl.torch(dev)
+
+    def call():
+        return chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
+                                      initial_state=t["initial_state"], output_final_state=True,
+                                      cu_seqlens=t["cu_seqlens"])
+    call()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    times = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        call()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1))
+    ms = float(np.median(times))
+    d = wl.dims
+    tokens = d["B"] * d["T"]
+    flops = prefill_flops(tokens, d["Hv"], d["K"], d["V"])
+    return {"workload": name, "tokens": tokens, "sequences": d["N"], "ms": round(ms, 3),
+            "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s",
+            "roofline_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+
 def bench_decode(dev, nsteps=1000, pool=10):
     from avelang_amd import fused_recurrent_gated_delta_rule
     from avelang_amd import workloads as W
@@ -353,6 +386,7 @@ def main():
     dec = bench_decode(dev, args.decode_steps)
     layer = None if args.no_layer_ops else bench_layer_ops(dev)
     pre_l2 = bench_prefill(dev, max(args.steps // 2, 1), args.warmup, l2norm=True)
+    others = [bench_prefill_config(dev, n) for n in ("cfg3_varlen_64seq", "cfg4_long_context")]
 
     flops = prefill_flops(pre["T"], pre["Hv"], pre["K"], pre["V"])
     tflops = flops / (pre["ms"] * 1e-3) / 1e12
@@ -402,6 +436,7 @@ def main():
             "workload": "cfg1 as the layer calls it: use_qk_l2norm_in_kernel=True (q, k normalised inside)",
             "value": round(pre_l2["T"] / (pre_l2["ms"] * 1e-3), 1), "unit": "tokens/s",
             "ms_per_step": round(pre_l2["ms"], 5)},
+        "prefill_other_configs": others,
         "layer_ops": layer,
         "host_wall_ms_per_step": round(pre["wall_ms"], 5),
     }

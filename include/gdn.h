@@ -59,8 +59,6 @@ extern "C" {
  *       ht may equal h0 (in-place update); any other overlap is an error.
  *   use_qk_l2norm != 0: q and k are L2-normalised over K (eps 1e-6) and
  *       rounded to bf16 before use.
- *   max_tokens_per_seq: host-side upper bound of the longest sequence
- *       (T when cu_seqlens is NULL); only sizes the launch grid.
  *   workspace: device scratch of at least gdn_chunk_workspace_bytes(...).
  */
 int gdn_chunk_fwd(const void* q, const void* k, const void* v,
