@@ -6,11 +6,14 @@
 // has no GDN code, its launcher convention is backends/amdgpu/driver.py:
 // 324-343 (raw pointers + scalars + caller stream).
 //
-// Design: the path is HBM-bound (0.8 flop/B), so there is no MFMA.  One
-// workgroup of NT lanes owns one (sequence, v-head) state tile S[K][V]
-// (fp32, 64 KiB at K = V = 128, where NT = 512: measured on MI355X, 512
-// lanes x 8 float4 per 64 KiB tile streams an in-place read-modify-write at
-// ~6.0 TB/s against ~5.35 TB/s for 256 lanes x 16).  Each lane holds a
+// Design: the path is HBM-bound (0.8 flop/B), so there is no MFMA.  A
+// workgroup of NT lanes advances one (sequence, v-head) state tile S[K][V]
+// at a time (fp32, 64 KiB at K = V = 128, where NT = 512: measured on
+// MI355X, 512 lanes x 8 float4 per 64 KiB tile streams an in-place
+// read-modify-write faster than 256 lanes x 16), and a persistent grid of
+// 1024 workgroups (4 per CU) walks the tiles with the next tile's state
+// loaded while the current one is advanced: 6.27 TB/s at batch 256 against
+// 5.35 TB/s for one workgroup per tile.  Each lane holds a
 // float4 column group of K/ROWG rows in VGPRs; the tile is read once with
 // coalesced 16-byte nontemporal loads (a wavefront covers whole contiguous
 // rows), advanced through every token of the sequence in registers, and
@@ -26,6 +29,20 @@
 
 namespace gdn {
 
+// Cache-policy bits of a raw buffer access on gfx950: NT (streaming).
+constexpr int kNonTemporal = 2;
+#ifndef GDN_DECODE_GRID
+#define GDN_DECODE_GRID 1024
+#endif
+// workgroups of the persistent decode grid
+constexpr int kDecodeGrid = GDN_DECODE_GRID;
+
+// Persistent form: a workgroup walks tiles blockIdx.x, +G, +2G, ... and
+// loads the next tile's state while it advances the current one, so the
+// state stream never waits for the per-token reductions.  State loads go
+// through a buffer resource whose size is 0 for a tile that has nothing to
+// load (past the end, padding slot, no h0): those loads return zeros and
+// touch no memory, so the prefetch needs no branch.
 template <int K, int V, int NT>
 __global__ __launch_bounds__(NT) void recurrent_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -33,7 +50,7 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     const float* __restrict__ beta, const float* h0, float* ht,
     uint16_t* __restrict__ o, const int32_t* __restrict__ cu, int T,
     int total_tokens, int Hqk, int Hv, float scale, int l2norm,
-    const int32_t* __restrict__ slots, int num_slots) {
+    const int32_t* __restrict__ slots, int num_slots, int ntiles) {
   constexpr int COLG = V / 4;          // float4 column groups per row
   constexpr int ROWG = NT / COLG;      // row groups
   constexpr int RPT = K / ROWG;        // rows per lane
@@ -50,115 +67,138 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
   const int rg = tid / COLG;
   const int wave = tid / 64;
   const int lane = tid % 64;
-  const int h = blockIdx.x % Hv;
-  const int n = blockIdx.x / Hv;
-  const int hq = h / (Hv / Hqk);
+  const int G = gridDim.x;
 
-  int s, e;
-  if (cu) {
-    s = min(max(cu[n], 0), total_tokens);
-    e = min(max(cu[n + 1], s), total_tokens);
-  } else {
-    s = n * T;
-    e = s + T;
-  }
-
-  // state slot of sequence n (a pool of slots under continuous batching;
-  // a slot outside the pool marks a padding sequence, left untouched)
-  int slot = n;
-  if (slots) {
-    slot = slots[n];
-    if (slot < 0 || slot >= num_slots) return;
-  }
-  const size_t tile = ((size_t)slot * Hv + h) * (size_t)K * V;
-  f32x4 S[RPT];
-  if (h0) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(h0 + tile);
+  // state slot of tile (sequence n, v-head h); under continuous batching a
+  // slot outside the pool marks a padding sequence, left untouched
+  auto slot_of = [&](int tile) {
+    const int n = tile / Hv;
+    int slot = n;
+    if (slots) {
+      slot = slots[n];
+      if (slot < 0 || slot >= num_slots) slot = -1;
+    }
+    return slot;
+  };
+  auto load_state = [&](f32x4 (&S)[RPT], int tile) {
+    const int tl = min(tile, ntiles - 1);
+    const int slot = slot_of(tl);
+    const bool live = h0 && tile < ntiles && slot >= 0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(h0) + (live ? ((size_t)slot * Hv + tl % Hv) * (size_t)K * V : 0), 0,
+        live ? K * V * 4 : 0, kBufferFlags);
 #pragma unroll
     for (int i = 0; i < RPT; ++i)
-      S[i] = __builtin_nontemporal_load(src + (size_t)(rg + ROWG * i) * COLG + cg);
-  } else {
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) S[i] = zero4();
-  }
+      S[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+          rs, ((rg + ROWG * i) * COLG + cg) * 16, 0, kNonTemporal));
+  };
 
-  for (int t = s; t < e; ++t) {
-    const size_t qk_row = ((size_t)t * Hqk + hq) * K;
-    if (tid < K) {
-      kq_s[0][tid] = bf2f(k[qk_row + tid]);
-      kq_s[1][tid] = bf2f(q[qk_row + tid]);
+  auto run_tile = [&](f32x4 (&S)[RPT], int tile) {
+    const int slot = slot_of(tile);
+    if (slot < 0) return;
+    const int h = tile % Hv;
+    const int n = tile / Hv;
+    const int hq = h / (Hv / Hqk);
+    int s, e;
+    if (cu) {
+      s = min(max(cu[n], 0), total_tokens);
+      e = min(max(cu[n + 1], s), total_tokens);
+    } else {
+      s = n * T;
+      e = s + T;
     }
-    const size_t vh = (size_t)t * Hv + h;
-    const u16x4 vb = *reinterpret_cast<const u16x4*>(v + vh * V + 4 * cg);
-    const float gt = g[vh];
-    const float bt = beta[vh];
-    __syncthreads();
+    for (int t = s; t < e; ++t) {
+      const size_t qk_row = ((size_t)t * Hqk + hq) * K;
+      if (tid < K) {
+        kq_s[0][tid] = bf2f(k[qk_row + tid]);
+        kq_s[1][tid] = bf2f(q[qk_row + tid]);
+      }
+      const size_t vh = (size_t)t * Hv + h;
+      const u16x4 vb = *reinterpret_cast<const u16x4*>(v + vh * V + 4 * cg);
+      const float gt = g[vh];
+      const float bt = beta[vh];
+      __syncthreads();
 
-    float r[NRED];
-    float kreg[RPT];  // k rows kept in VGPRs: kq_s is restaged by the next token
+      float r[NRED];
+      float kreg[RPT];  // k rows kept in VGPRs: kq_s is restaged by the next token
 #pragma unroll
-    for (int j = 0; j < NRED; ++j) r[j] = 0.f;
+      for (int j = 0; j < NRED; ++j) r[j] = 0.f;
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const float kr = kq_s[0][rg + ROWG * i];
-      const float qr = kq_s[1][rg + ROWG * i];
-      kreg[i] = kr;
+      for (int i = 0; i < RPT; ++i) {
+        const float kr = kq_s[0][rg + ROWG * i];
+        const float qr = kq_s[1][rg + ROWG * i];
+        kreg[i] = kr;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          r[c] += S[i][c] * kr;
+          r[4 + c] += S[i][c] * qr;
+        }
+        r[8] += kr * qr;
+        r[9] += kr * kr;
+        r[10] += qr * qr;
+      }
+#pragma unroll
+      for (int off = COLG; off < 64; off *= 2) {
+#pragma unroll
+        for (int j = 0; j < NRED; ++j) r[j] += __shfl_xor(r[j], off);
+      }
+      if (lane < COLG) {
+#pragma unroll
+        for (int j = 0; j < NRED; ++j) red[wave][cg][j] = r[j];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < NRED; ++j) {
+        float acc = red[0][cg][j];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) acc += red[ww][cg][j];
+        r[j] = acc;
+      }
+
+      const float ik = l2norm ? rsqrtf(r[9] + 1e-6f) : 1.f;
+      const float iq = l2norm ? rsqrtf(r[10] + 1e-6f) : 1.f;
+      const float eg = __expf(gt);
+      float d[4];
+      float ov[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        r[c] += S[i][c] * kr;
-        r[4 + c] += S[i][c] * qr;
+        d[c] = bt * (bf2f(vb[c]) - eg * r[c] * ik);
+        ov[c] = scale * iq * (eg * r[4 + c] + d[c] * r[8] * ik);
       }
-      r[8] += kr * qr;
-      r[9] += kr * kr;
-      r[10] += qr * qr;
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const float kr = kreg[i] * ik;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) S[i][c] = eg * S[i][c] + kr * d[c];
+      }
+      if (rg == 0) {
+        u16x4 ob;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ob[c] = f2bf(ov[c]);
+        *reinterpret_cast<u16x4*>(o + vh * V + 4 * cg) = ob;
+      }
     }
+    if (ht) {
+      f32x4* dst = reinterpret_cast<f32x4*>(ht + ((size_t)slot * Hv + h) * (size_t)K * V);
 #pragma unroll
-    for (int off = COLG; off < 64; off *= 2) {
-#pragma unroll
-      for (int j = 0; j < NRED; ++j) r[j] += __shfl_xor(r[j], off);
+      for (int i = 0; i < RPT; ++i)
+        __builtin_nontemporal_store(S[i], dst + (size_t)(rg + ROWG * i) * COLG + cg);
     }
-    if (lane < COLG) {
-#pragma unroll
-      for (int j = 0; j < NRED; ++j) red[wave][cg][j] = r[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < NRED; ++j) {
-      float acc = red[0][cg][j];
-#pragma unroll
-      for (int ww = 1; ww < NW; ++ww) acc += red[ww][cg][j];
-      r[j] = acc;
-    }
+  };
 
-    const float ik = l2norm ? rsqrtf(r[9] + 1e-6f) : 1.f;
-    const float iq = l2norm ? rsqrtf(r[10] + 1e-6f) : 1.f;
-    const float eg = __expf(gt);
-    float d[4];
-    float ov[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      d[c] = bt * (bf2f(vb[c]) - eg * r[c] * ik);
-      ov[c] = scale * iq * (eg * r[4 + c] + d[c] * r[8] * ik);
-    }
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const float kr = kreg[i] * ik;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) S[i][c] = eg * S[i][c] + kr * d[c];
-    }
-    if (rg == 0) {
-      u16x4 ob;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) ob[c] = f2bf(ov[c]);
-      *reinterpret_cast<u16x4*>(o + vh * V + 4 * cg) = ob;
-    }
-  }
-
-  if (ht) {
-    f32x4* dst = reinterpret_cast<f32x4*>(ht + tile);
-#pragma unroll
-    for (int i = 0; i < RPT; ++i)
-      __builtin_nontemporal_store(S[i], dst + (size_t)(rg + ROWG * i) * COLG + cg);
+  int t = blockIdx.x;
+  if (t >= ntiles) return;
+  f32x4 SA[RPT], SB[RPT];
+  load_state(SA, t);
+  for (;;) {
+    load_state(SB, t + G);
+    run_tile(SA, t);
+    t += G;
+    if (t >= ntiles) break;
+    load_state(SA, t + G);
+    run_tile(SB, t);
+    t += G;
+    if (t >= ntiles) break;
   }
 }
 
@@ -170,9 +210,13 @@ static void launch_recurrent(const uint16_t* q, const uint16_t* k, const uint16_
                              const int32_t* slots, int num_slots, hipStream_t stream) {
   const int total_tokens = B * T;
   constexpr int NT = (K * V >= 128 * 128) ? 512 : 256;
-  hipLaunchKernelGGL((recurrent_kernel<K, V, NT>), dim3(N * Hv), dim3(NT), 0, stream, q, k, v,
+  const int ntiles = N * Hv;
+  // persistent workgroups: enough to fill every CU several times over, each
+  // walking ntiles / grid tiles with the next state prefetched
+  const int grid = ntiles < kDecodeGrid ? ntiles : kDecodeGrid;
+  hipLaunchKernelGGL((recurrent_kernel<K, V, NT>), dim3(grid), dim3(NT), 0, stream, q, k, v,
                      g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm, slots,
-                     num_slots);
+                     num_slots, ntiles);
 }
 
 }  // namespace gdn
