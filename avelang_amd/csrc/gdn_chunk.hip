@@ -35,7 +35,7 @@ namespace gdn {
 // ---------------------------------------------------------------- layout --
 struct ChunkWs {
   int32_t* off;     // [N+1] first global chunk of each sequence
-  float* gate;      // [NC][Hv][128]: e^G_i (64), then e^(G_last - G_i) (64)
+  float* gate;      // [NC][Hv][64]: G_i, the chunk-local cumulative log-decay
   u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
   u16x8* pfrag;     // [NC][Hv][4][2][64]
   uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] (use_qk_l2norm only),
@@ -204,10 +204,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       const float o = __shfl_up(gv, d);
       if (lane >= d) gv += o;
     }
-    const float gl = __shfl(gv, L - 1);
-    float* gate = ws.gate + ((size_t)ci * Hv + h) * 128;
-    gate[lane] = __expf(gv);
-    gate[64 + lane] = __expf(gl - gv);
+    ws.gate[((size_t)ci * Hv + h) * 64 + lane] = gv;
     Gs[lane] = gv;
     Bs[lane] = bv;
   }
@@ -368,8 +365,7 @@ struct ChainIn {
   u16x8 tf[2][2];         // Tb rows [k-block][hi, lo]
   u16x8 pf[2];            // P rows [k-block]
   uint16_t vv[4];         // V[row 4grp+r][16 vt + r16], raw bf16
-  f32x4 eg, dec;          // e^G_row, e^(G_last - G_row) for rows 4grp+r
-  float egl;              // e^G_last
+  float G;                // G of row `lane` (rows >= L repeat G_last)
 };
 
 struct ChainCtx {
@@ -428,11 +424,9 @@ __device__ __forceinline__ void chain_load_c(ChainIn<K>& in, const ChainCtx& c, 
 #pragma unroll
   for (int r = 0; r < 4; ++r)
     in.vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, c.v_off + r * rowb, 0, 0);
-  const float* gate = c.ws.gate + ((size_t)ci * c.Hv + c.h) * 128;
-  const int grp = c.lane / 16;
-  in.eg = *reinterpret_cast<const f32x4*>(gate + 16 * c.w + 4 * grp);
-  in.dec = *reinterpret_cast<const f32x4*>(gate + 64 + 16 * c.w + 4 * grp);
-  in.egl = gate[L - 1];
+  // one 4-byte load per lane (row `lane`) instead of the per-row factors
+  // in MFMA output layout: the step forms e^G and e^(G_last - G) itself
+  in.G = c.ws.gate[((size_t)ci * c.Hv + c.h) * 64 + c.lane];
 }
 
 template <int K>
@@ -509,6 +503,18 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
     chain_load_a<K>(nxt, ctx, cn);
+    // gate factors of this wave's rows 16w + 4grp + r: e^G, e^(G_last - G),
+    // and e^G_last (row L - 1), from the one G value each lane loaded
+    f32x4 eg, dec;
+    const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.G), L - 1));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float Gr = __int_as_float(
+          __builtin_amdgcn_ds_bpermute((16 * w + 4 * grp + r) * 4, __float_as_int(cur.G)));
+      eg[r] = __expf(Gr);
+      dec[r] = __expf(GL - Gr);
+    }
+    const float egl = __expf(GL);
     const u16x8* kf = cur.kf;
     const u16x8* qf = cur.qf;
     // stage this chunk's K rows for the K^T operand of the state update
@@ -534,7 +540,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       u16x4 yh, yl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float y = bf2f(cur.vv[r]) - cur.eg[r] * X[r];
+        const float y = bf2f(cur.vv[r]) - eg[r] * X[r];
         uint16_t a, b;
         split_bf(y, a, b);
         yh[r] = a;
@@ -589,7 +595,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         uint16_t a, b;
-        split_bf(cur.dec[r] * vn[r], a, b);
+        split_bf(dec[r] * vn[r], a, b);
         uh[r] = a;
         ul[r] = b;
         vb[r] = f2bf(vn[r]);
@@ -611,7 +617,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       }
 #pragma unroll
       for (int tt = 0; tt < RT; ++tt) {
-        f32x4 a0 = Sr[tt] * cur.egl, a1 = zero4();
+        f32x4 a0 = Sr[tt] * egl, a1 = zero4();
         a0 = mfma16(ka[tt][0], uh[0], a0);
         a1 = mfma16(ka[tt][0], ul[0], a1);
         a0 = mfma16(ka[tt][1], uh[1], a0);
@@ -634,7 +640,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * w + 4 * grp + r;
-        __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * cur.eg[r] * QS[r] + (oa[r] + ob[r])),
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * eg[r] * QS[r] + (oa[r] + ob[r])),
                                               orsrc, ((row * Hv + h) * V + 16 * vt + r16) * 2,
                                               0, 0);
       }
@@ -687,7 +693,7 @@ static WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int N, bool has_cu, 
   p.off = at;
   at = align256(at + (size_t)(N + 1) * 4);
   p.gate = at;
-  at = align256(at + (size_t)p.ncmax * Hv * 128 * 4);
+  at = align256(at + (size_t)p.ncmax * Hv * 64 * 4);
   p.tfrag = at;
   at = align256(at + (size_t)p.ncmax * Hv * 4 * 2 * 2 * 64 * 16);
   p.pfrag = at;
