@@ -259,9 +259,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     if (tc < w) *reinterpret_cast<f32x4*>(&Af[i * kLdA + 16 * tc + 4 * grp]) = av;
     // P fragment slot: k-block tc/2, fragment lane r16 + 16 (2 (tc%2) + grp/2),
     // elements 4 (grp%2) .. +3
-    const size_t pf = (pbase + tc / 2) * 64 + r16 + 16 * (2 * (tc % 2) + grp / 2);
-    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(ws.pfrag + pf) + 4 * (grp % 2)) =
-        __builtin_bit_cast(u32x2, pv);
+    // (k-block 1 of row tiles 0 and 1 is zero and never read: not stored)
+    if (tc < 2 || w >= 2) {
+      const size_t pf = (pbase + tc / 2) * 64 + r16 + 16 * (2 * (tc % 2) + grp / 2);
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(ws.pfrag + pf) + 4 * (grp % 2)) =
+          __builtin_bit_cast(u32x2, pv);
+    }
   }
   __syncthreads();
 
@@ -320,6 +323,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int row = 16 * w + r16;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
+    if (b == 1 && w < 2) break;   // zero block, never read by the chain
     const int c0 = 32 * b + 8 * grp;
     const f32x4 t0v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0]);
     const f32x4 t1v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0 + 4]);
@@ -405,11 +409,20 @@ __device__ __forceinline__ void chain_load_b(ChainIn<K>& in, const ChainCtx& c, 
   const size_t base = ((size_t)ci * c.Hv + c.h) * 4 + c.w;
   const u16x8* tb = c.ws.tfrag + base * 256;
   const u16x8* pb = c.ws.pfrag + base * 128;
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    in.tf[b][0] = tb[(b * 2 + 0) * 64 + c.lane];
-    in.tf[b][1] = tb[(b * 2 + 1) * 64 + c.lane];
-    in.pf[b] = pb[b * 64 + c.lane];
+  in.tf[0][0] = tb[c.lane];
+  in.tf[0][1] = tb[64 + c.lane];
+  in.pf[0] = pb[c.lane];
+  // k-block 1 (columns 32..63) of row tiles 0 and 1 is zero in both Tb and
+  // P (lower triangular): those waves skip the loads (a wave-uniform branch)
+  if (c.w >= 2) {
+    in.tf[1][0] = tb[128 + c.lane];
+    in.tf[1][1] = tb[192 + c.lane];
+    in.pf[1] = pb[64 + c.lane];
+  } else {
+    const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+    in.tf[1][0] = z;
+    in.tf[1][1] = z;
+    in.pf[1] = z;
   }
 }
 
