@@ -367,6 +367,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-layer-ops", action="store_true",
                     help="skip the layer-operator measurements")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the config-1 prefill and config-2 decode lines (profiling runs)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run the fixed untimed launch sequence used for rocprofv3 --pmc runs")
     args = ap.parse_args()
@@ -384,9 +386,11 @@ def main():
 
     pre = bench_prefill(dev, args.steps, args.warmup)
     dec = bench_decode(dev, args.decode_steps)
-    layer = None if args.no_layer_ops else bench_layer_ops(dev)
-    pre_l2 = bench_prefill(dev, max(args.steps // 2, 1), args.warmup, l2norm=True)
-    others = [bench_prefill_config(dev, n) for n in ("cfg3_varlen_64seq", "cfg4_long_context")]
+    extra = not args.headline_only
+    layer = bench_layer_ops(dev) if extra and not args.no_layer_ops else None
+    pre_l2 = bench_prefill(dev, max(args.steps // 2, 1), args.warmup, l2norm=True) if extra else None
+    others = ([bench_prefill_config(dev, n) for n in ("cfg3_varlen_64seq", "cfg4_long_context")]
+              if extra else None)
 
     flops = prefill_flops(pre["T"], pre["Hv"], pre["K"], pre["V"])
     tflops = flops / (pre["ms"] * 1e-3) / 1e12
@@ -432,7 +436,7 @@ def main():
                          "algorithmic_bytes_per_launch": dec["bytes"]},
             "cpu_baseline": cpu_dec,
         },
-        "prefill_qk_l2norm_in_kernel": {
+        "prefill_qk_l2norm_in_kernel": None if pre_l2 is None else {
             "workload": "cfg1 as the layer calls it: use_qk_l2norm_in_kernel=True (q, k normalised inside)",
             "value": round(pre_l2["T"] / (pre_l2["ms"] * 1e-3), 1), "unit": "tokens/s",
             "ms_per_step": round(pre_l2["ms"], 5)},
