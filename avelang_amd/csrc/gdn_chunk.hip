@@ -347,9 +347,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 
 // --------------------------------------------------------- chain (K2) ----
 // Operands of one chunk step for wave w (chunk rows 16w..16w+15), fetched one
-// step ahead in three parts so the vector-memory queue never stalls a wave
-// for long: A (K and Q rows) before the K S products, B (Tb, P fragments)
-// after the first barrier, C (V column slice, gate factors) after the second.
+// step ahead in parts so the vector-memory queue never stalls a wave for
+// long: A (K rows) before the K S products, B (Tb, P fragments) and Q rows
+// after the first barrier, C (V column slice, G) after the second.
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
@@ -395,13 +395,24 @@ __device__ __forceinline__ void chain_load_a(ChainIn<K>& in, const ChainCtx& c, 
   const int bytes = L * c.Hqk * K * 2;
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(c.k + row0 * K), 0, bytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(c.q + row0 * K), 0, bytes, kBufferFlags);
 #pragma unroll
-  for (int b = 0; b < ChainIn<K>::KB; ++b) {
+  for (int b = 0; b < ChainIn<K>::KB; ++b)
     in.kf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, c.kq_off + 64 * b, 0, 0));
+}
+
+// Q rows: issued after the first barrier with the Tb / P fragments, which
+// spreads the prefetch over the step (issued together with the K rows they
+// made the first phase wait on the vector-memory queue).
+template <int K>
+__device__ __forceinline__ void chain_load_q(ChainIn<K>& in, const ChainCtx& c, int ci) {
+  const int t0 = c.s + (ci - c.c_begin) * kChunk;
+  const int L = min(kChunk, c.e - t0);
+  const size_t row0 = (size_t)t0 * c.Hqk + c.hq;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(c.q + row0 * K), 0, L * c.Hqk * K * 2, kBufferFlags);
+#pragma unroll
+  for (int b = 0; b < ChainIn<K>::KB; ++b)
     in.qf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, c.kq_off + 64 * b, 0, 0));
-  }
 }
 
 template <int K>
@@ -564,6 +575,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     }
     __syncthreads();
     chain_load_b<K>(nxt, ctx, cn);
+    chain_load_q<K>(nxt, ctx, cn);
 
     // K^T fragments of the update, gathered now (off the critical path):
     // element ii of lane (r16, grp) is Kl[32b + 8grp + ii][kd0 + r16], two
@@ -670,6 +682,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   if (c_begin < c_end) {
     chain_load_a<K>(bufA, ctx, c_begin);
     chain_load_b<K>(bufA, ctx, c_begin);
+    chain_load_q<K>(bufA, ctx, c_begin);
     chain_load_c<K>(bufA, ctx, c_begin);
   }
   for (int ci = c_begin; ci < c_end; ci += 2) {
