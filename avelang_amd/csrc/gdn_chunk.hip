@@ -592,13 +592,16 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
         ka[tt][b] = u16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
       }
     }
-    // QS = Q S_hi (needed only for o; S is republished in the last phase)
+    // (Q S_hi)^T = S_hi^T Q^T (needed only for o; S is republished in the
+    // last phase).  The output is formed transposed so that each lane ends
+    // with 4 consecutive columns of one row: one 8-byte store instead of four
+    // 2-byte stores.  The operands are the same fragments, swapped.
     f32x4 qa = zero4(), qb = zero4();
 #pragma unroll
     for (int b = 0; b < KB; b += 2) {
-      qa = mfma16(qf[b], *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]), qa);
-      qb = mfma16(qf[b + 1],
-                  *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]), qb);
+      qa = mfma16(*reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]), qf[b], qa);
+      qb = mfma16(*reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]),
+                  qf[b + 1], qb);
     }
 
     // vnew = Tb Y (three hi/lo terms, independent accumulators)
@@ -650,25 +653,28 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
         Sr[tt] = a0 + a1;
       }
     }
-    // o = scale e^G (Q S) + P vnew
+    // o^T = scale e^G (Q S)^T + vnew^T P^T: lane holds row 16w + r16,
+    // columns 16 vt + 4 grp .. + 3
     {
       const u16x8 v0 = *reinterpret_cast<const u16x8*>(&VnT[r16][8 * grp]);
       const u16x8 v1 = *reinterpret_cast<const u16x8*>(&VnT[r16][32 + 8 * grp]);
-      const f32x4 oa = mfma16(cur.pf[0], v0, zero4());
-      const f32x4 ob = mfma16(cur.pf[1], v1, zero4());
+      const f32x4 oa = mfma16(v0, cur.pf[0], zero4());
+      const f32x4 ob = mfma16(v1, cur.pf[1], zero4());
       const f32x4 QS = qa + qb;
-      // Buffer stores bounded to this chunk's L rows: the hardware drops the
+      const float egi = __expf(__int_as_float(
+          __builtin_amdgcn_ds_bpermute((16 * w + r16) * 4, __float_as_int(cur.G))));
+      u16x4 ov;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ov[r] = f2bf(scale * egi * QS[r] + (oa[r] + ob[r]));
+      // Buffer store bounded to this chunk's L rows: the hardware drops the
       // padding rows, so the store needs no branch (a branch here would make
       // the compiler wait for every outstanding load at the loop head).
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
           o + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * grp + r;
-        __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * eg[r] * QS[r] + (oa[r] + ob[r])),
-                                              orsrc, ((row * Hv + h) * V + 16 * vt + r16) * 2,
-                                              0, 0);
-      }
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      __builtin_amdgcn_raw_buffer_store_b64(
+          __builtin_bit_cast(u32x2, ov), orsrc,
+          (((16 * w + r16) * Hv + h) * V + 16 * vt + 4 * grp) * 2, 0, 0);
     }
     publish_state();
     __syncthreads();
