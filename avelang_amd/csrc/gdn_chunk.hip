@@ -471,9 +471,21 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t Kl[64][LDS_];
 
   const int NVT = V / 16;
+  // Workgroups are dealt to the 8 XCDs round-robin by blockIdx.  The unit
+  // kept on one XCD is a qk-head group (its G v-heads x NVT tiles share K, Q
+  // and the Tb / P fragments through that XCD's L2), and the units are dealt
+  // round-robin too, so every XCD gets 1/8 of every sequence: with packed
+  // sequences of unequal length, contiguous ranges per XCD left some XCDs
+  // with much more work than others.
   int bid = blockIdx.x;
   const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);  // one head's tiles per XCD
+  const int unit = NVT * (Hv / Hqk);
+  if (nb % (8 * unit) == 0) {
+    const int i = bid >> 3;
+    bid = ((i / unit) * 8 + (bid & 7)) * unit + i % unit;
+  } else if ((nb & 7) == 0) {
+    bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  }
   const int vt = bid % NVT;
   const int h = (bid / NVT) % Hv;
   const int n = bid / NVT / Hv;
