@@ -144,6 +144,14 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
   const int r16 = lane % 16, grp = lane / 16;
 
+  // g and beta of the chunk's rows (wave 0), issued first so that their
+  // latency overlaps that of the K / Q rows rather than following it
+  float gv = 0.f, bv = 0.f;
+  if (w == 0) {
+    const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
+    gv = g[grow];
+    bv = beta[grow];
+  }
   // K / Q rows straight into MFMA fragments (this wave's rows); the K rows
   // are also staged in LDS, where the other waves read them as B operands.
   // Padding rows (row >= L) repeat row L-1: their A rows are scaled by
@@ -195,8 +203,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   // gates: wave 0 scans g over the 64 rows (padding rows add 0) and shares
   // G and beta through LDS
   if (w == 0) {
-    const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
-    float gv = g[grow], bv = beta[grow];
     gv = lane < L ? gv : 0.f;
     bv = lane < L ? bv : 0.f;
 #pragma unroll
