@@ -98,8 +98,8 @@ def test_workspace_bytes_grow_with_problem(lib):
     c = f(1, 8192, 16, 32, 128, 128, 64, 1, 0)
     d = f(1, 8192, 16, 32, 128, 128, 1, 0, 1)
     assert 0 < a < b and c > a and d > a
-    # per (chunk, v-head): 128 gate floats + 16 KiB Tb + 8 KiB P fragments
-    assert a >= 128 * 32 * (512 + 16384 + 8192)
+    # per (chunk, v-head): 64 gate floats (G) + 16 KiB Tb + 8 KiB P fragments
+    assert a >= 128 * 32 * (256 + 16384 + 8192)
 
 
 def test_empty_problem_is_a_noop(lib):

@@ -109,6 +109,14 @@ def test_decode_head_sizes(rocm_device, K, V):
     _check(o, o_ref, s, s_ref, f"decode K={K} V={V}")
 
 
+@pytest.mark.parametrize("Hqk,Hv", [(8, 8), (2, 8)])
+def test_decode_gqa_ratios(rocm_device, Hqk, Hv):
+    wl = W.make(6, 2, Hqk, Hv, 128, 128, seed=Hqk + 10 * Hv, h0_scale=0.01)
+    o_ref, s_ref = _oracle("recurrent", wl)
+    o, s = _run_rec(wl, rocm_device)
+    _check(o, o_ref, s, s_ref, f"decode Hqk={Hqk} Hv={Hv}")
+
+
 def test_decode_varlen_with_empty(rocm_device):
     cu = np.array([0, 3, 3, 4, 10, 10, 17], np.int32)
     wl = W.make(1, 17, 4, 8, 128, 128, seed=9, h0_scale=0.01, cu_seqlens=cu)
@@ -147,6 +155,24 @@ def test_prefill_head_sizes(rocm_device, K, V):
     o_ref, s_ref = _oracle("chunk", wl)
     o, s = _run_chunk(wl, rocm_device)
     _check(o, o_ref, s, s_ref, f"prefill K={K} V={V}")
+
+
+# (Hqk, Hv, B, V): G = Hv / Hqk of 1, 2 and 4.  The chain deals workgroups to
+# the XCDs in units of one qk-head group (G v-heads x V/16 tiles) when the
+# grid holds a multiple of 8 units, else in contiguous ranges: the cases
+# cover both mappings (grid 128, 256 and 64 workgroups).
+@pytest.mark.parametrize("Hqk,Hv,B,V", [(8, 8, 2, 128), (2, 8, 4, 128), (4, 8, 2, 64),
+                                        (2, 4, 2, 128)])
+@pytest.mark.parametrize("l2", [False, True])
+def test_prefill_gqa_ratios(rocm_device, Hqk, Hv, B, V, l2):
+    wl = W.make(B, 130, Hqk, Hv, 128, V, seed=Hqk * 7 + Hv + B + V, h0_scale=0.01, l2norm=not l2)
+    a = wl.numpy()
+    if l2:
+        nrm = lambda x: x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-6)  # noqa: E731
+        a["q"], a["k"] = W._bf16_round(nrm(a["q"])), W._bf16_round(nrm(a["k"]))
+    o_ref, s_ref = oracle.run("chunk", **a)
+    o, s = _run_chunk(wl, rocm_device, use_qk_l2norm_in_kernel=l2)
+    _check(o, o_ref, s, s_ref, f"prefill Hqk={Hqk} Hv={Hv} B={B} V={V} l2={l2}")
 
 
 def test_prefill_cfg1_full(rocm_device):
