@@ -105,7 +105,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, float scale,
     int l2norm, ChunkWs ws) {
   constexpr int KB = K / 32;
-  __shared__ __attribute__((aligned(16))) float Af[64 * kLdA];
+  // strictly lower 16 x 16 blocks of A only (block (bi, m), m < bi, at
+  // bi (bi - 1) / 2 + m; row stride 20 keeps float4 rows aligned and the 16
+  // rows of a read on distinct banks): 7.5 KB instead of a full 64 x 68
+  // array, which lets 5 workgroups share a CU instead of 4
+  __shared__ __attribute__((aligned(16))) float Ab[6][16][20];
   __shared__ __attribute__((aligned(16))) float Tm[64 * kLdA];
   // The chunk's K rows are staged in Tm's space until K K^T is formed.
   static_assert(64 * (K + 8) * 2 <= 64 * kLdA * 4, "K staging must fit in Tm");
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       av[r] = (j < i) ? Bi * kt[r] * gam : 0.f;
       pv[r] = f2bf(scale * pt[r] * gam);
     }
-    if (tc < w) *reinterpret_cast<f32x4*>(&Af[i * kLdA + 16 * tc + 4 * grp]) = av;
+    if (tc < w) *reinterpret_cast<f32x4*>(&Ab[w * (w - 1) / 2 + tc][r16][4 * grp]) = av;
     // P fragment slot: k-block tc/2, fragment lane r16 + 16 (2 (tc%2) + grp/2),
     // elements 4 (grp%2) .. +3
     // (k-block 1 of row tiles 0 and 1 is zero and never read: not stored)
@@ -309,7 +313,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     if (bi < 4) {
       f32x4 acc = zero4();
       for (int m = bj; m < bi; ++m) {
-        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Af[(16 * bi + r16) * kLdA + 16 * m + 4 * grp]);
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&Ab[bi * (bi - 1) / 2 + m][r16][4 * grp]);
         const float* tb = &Tm[(16 * m + 4 * grp) * kLdA + 16 * bj + r16];
 #pragma unroll
         for (int st = 0; st < 4; ++st) acc = mfma4f32(a4[st], tb[st * kLdA], acc);
