@@ -527,13 +527,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 #pragma unroll
     for (int tt = 0; tt < RT; ++tt) {
       u16x4 hi4, lo4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint16_t a, b;
-        split_bf(Sr[tt][r], a, b);
-        hi4[r] = a;
-        lo4[r] = b;
-      }
+      split_bf4(Sr[tt], hi4, lo4);
       const int kd0 = w * 16 * RT + 16 * tt + 4 * grp;
       *reinterpret_cast<u16x4*>(&SsT[0][r16][kd0]) = hi4;
       *reinterpret_cast<u16x4*>(&SsT[1][r16][kd0]) = lo4;
@@ -583,15 +577,11 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     }
     {
       const f32x4 X = (xa + xb) + (xc + xd);
-      u16x4 yh, yl;
+      f32x4 y;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float y = bf2f(cur.vv[r]) - eg[r] * X[r];
-        uint16_t a, b;
-        split_bf(y, a, b);
-        yh[r] = a;
-        yl[r] = b;
-      }
+      for (int r = 0; r < 4; ++r) y[r] = bf2f(cur.vv[r]) - eg[r] * X[r];
+      u16x4 yh, yl;
+      split_bf4(y, yh, yl);
       *reinterpret_cast<u16x4*>(&YsT[0][r16][16 * w + 4 * grp]) = yh;
       *reinterpret_cast<u16x4*>(&YsT[1][r16][16 * w + 4 * grp]) = yl;
     }
@@ -641,15 +631,9 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       vn = va + (vb + vc);
     }
     {
-      u16x4 uh, ul, vb;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint16_t a, b;
-        split_bf(dec[r] * vn[r], a, b);
-        uh[r] = a;
-        ul[r] = b;
-        vb[r] = f2bf(vn[r]);
-      }
+      u16x4 uh, ul;
+      split_bf4(dec * vn, uh, ul);
+      const u16x4 vb = f2bf4(vn);
       *reinterpret_cast<u16x4*>(&UsT[0][r16][16 * w + 4 * grp]) = uh;
       *reinterpret_cast<u16x4*>(&UsT[1][r16][16 * w + 4 * grp]) = ul;
       *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
@@ -685,9 +669,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       const f32x4 QS = qa + qb;
       const float egi = __expf(__int_as_float(
           __builtin_amdgcn_ds_bpermute((16 * w + r16) * 4, __float_as_int(cur.G))));
-      u16x4 ov;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ov[r] = f2bf(scale * egi * QS[r] + (oa[r] + ob[r]));
+      const u16x4 ov = f2bf4((scale * egi) * QS + (oa + ob));
       // Buffer store bounded to this chunk's L rows: the hardware drops the
       // padding rows, so the store needs no branch (a branch here would make
       // the compiler wait for every outstanding load at the loop head).

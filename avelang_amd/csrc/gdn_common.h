@@ -38,6 +38,22 @@ __device__ __forceinline__ void split_bf(float x, uint16_t& hi, uint16_t& lo) {
   lo = f2bf(x - bf2f(hi));
 }
 
+// Four values at once (two v_cvt_pk_bf16_f32 per conversion, and the hi
+// part re-expanded from the packed words with a shift / mask): the same
+// results as f2bf / split_bf per element, in fewer instructions.
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2p __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x4 f2bf4(f32x4 x) {
+  return __builtin_bit_cast(u16x4, __builtin_convertvector(x, bf16x4));
+}
+__device__ __forceinline__ void split_bf4(f32x4 x, u16x4& hi, u16x4& lo) {
+  const u32x2p hp = __builtin_bit_cast(u32x2p, __builtin_convertvector(x, bf16x4));
+  const f32x4 hf = {__uint_as_float(hp[0] << 16), __uint_as_float(hp[0] & 0xffff0000u),
+                    __uint_as_float(hp[1] << 16), __uint_as_float(hp[1] & 0xffff0000u)};
+  hi = __builtin_bit_cast(u16x4, hp);
+  lo = f2bf4(x - hf);
+}
+
 __device__ __forceinline__ bf16x8 as_bf(u16x8 v) {
   return __builtin_bit_cast(bf16x8, v);
 }
