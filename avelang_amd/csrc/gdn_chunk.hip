@@ -546,15 +546,17 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     // gate factors of this wave's rows 16w + 4grp + r: e^G, e^(G_last - G),
     // and e^G_last (row L - 1), from the one G value each lane loaded
     f32x4 eg, dec;
+    // (two exponentials per lane for its own row, then permuted: the same
+    // values as exponentials of permuted G, with 2 instead of 10 v_exp)
     const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.G), L - 1));
+    const float egx = __expf(cur.G), decx = __expf(GL - cur.G);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float Gr = __int_as_float(
-          __builtin_amdgcn_ds_bpermute((16 * w + 4 * grp + r) * 4, __float_as_int(cur.G)));
-      eg[r] = __expf(Gr);
-      dec[r] = __expf(GL - Gr);
+      const int src = (16 * w + 4 * grp + r) * 4;
+      eg[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(egx)));
+      dec[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(decx)));
     }
-    const float egl = __expf(GL);
+    const float egl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(egx), L - 1));
     const u16x8* kf = cur.kf;
     const u16x8* qf = cur.qf;
     // stage this chunk's K rows for the K^T operand of the state update
@@ -667,8 +669,8 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       const f32x4 oa = mfma16(v0, cur.pf[0], zero4());
       const f32x4 ob = mfma16(v1, cur.pf[1], zero4());
       const f32x4 QS = qa + qb;
-      const float egi = __expf(__int_as_float(
-          __builtin_amdgcn_ds_bpermute((16 * w + r16) * 4, __float_as_int(cur.G))));
+      const float egi = __int_as_float(
+          __builtin_amdgcn_ds_bpermute((16 * w + r16) * 4, __float_as_int(egx)));
       const u16x4 ov = f2bf4((scale * egi) * QS + (oa + ob));
       // Buffer store bounded to this chunk's L rows: the hardware drops the
       // padding rows, so the store needs no branch (a branch here would make
