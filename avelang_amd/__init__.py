@@ -1,7 +1,8 @@
 """avelang_amd — MI355X-native (gfx950) gated-delta-net hot path.
 
 Operators (FLA / Qwen3-Next argument lists):
-    chunk_gated_delta_rule            chunked prefill (chunk 64, MFMA)
+    chunk_gated_delta_rule            chunked prefill (chunk 64, MFMA), differentiable
+    chunk_gated_delta_rule_bwd        its gradients (q, k, v, g, beta, initial state)
     fused_recurrent_gated_delta_rule  token recurrence / decode (HBM-bound),
                                       optionally over a pool of state slots
 
@@ -13,7 +14,9 @@ All call hand-written HIP kernels through the C ABI in include/gdn.h and
 include/gdn_layer.h (``libgdn.so``, built by ``python -m avelang_amd.build``).
 """
 from .gated_delta_rule import (  # noqa: F401
+    chunk_bwd_workspace_bytes,
     chunk_gated_delta_rule,
+    chunk_gated_delta_rule_bwd,
     chunk_workspace_bytes,
     fused_recurrent_gated_delta_rule,
 )
@@ -27,8 +30,10 @@ from .layer_ops import (  # noqa: F401
 
 __all__ = [
     "chunk_gated_delta_rule",
+    "chunk_gated_delta_rule_bwd",
     "fused_recurrent_gated_delta_rule",
     "chunk_workspace_bytes",
+    "chunk_bwd_workspace_bytes",
     "fused_gdn_gating",
     "l2norm_fwd",
     "causal_conv1d_fn",

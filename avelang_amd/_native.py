@@ -19,6 +19,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libgdn.so"
 EXPORTS = (
     "gdn_chunk_fwd",
     "gdn_chunk_workspace_bytes",
+    "gdn_chunk_bwd",
+    "gdn_chunk_bwd_workspace_bytes",
     "gdn_recurrent_fwd",
     "gdn_last_error",
     "gdn_abi_version",
@@ -81,6 +83,17 @@ def lib():
         ]
         h.gdn_chunk_workspace_bytes.restype = _sz
         h.gdn_chunk_workspace_bytes.argtypes = [_i] * 9
+        h.gdn_chunk_bwd.restype = _i
+        h.gdn_chunk_bwd.argtypes = [
+            _vp, _vp, _vp, _vp, _vp, _vp,     # q k v g beta h0
+            _vp, _vp,                         # dO dht
+            _vp, _vp, _vp, _vp, _vp, _vp,     # dq dk dv dg dbeta dh0
+            _vp,                              # cu_seqlens
+            _i, _i, _i, _i, _i, _i, _i,       # B T Hqk Hv K V N
+            _f, _i, _vp, _sz, _vp,            # scale l2norm ws ws_bytes stream
+        ]
+        h.gdn_chunk_bwd_workspace_bytes.restype = _sz
+        h.gdn_chunk_bwd_workspace_bytes.argtypes = [_i] * 9
         h.gdn_recurrent_fwd.restype = _i
         h.gdn_recurrent_fwd.argtypes = [
             _vp, _vp, _vp, _vp, _vp,

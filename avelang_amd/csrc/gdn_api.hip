@@ -76,4 +76,4 @@ int validate_common(const void* q, const void* k, const void* v, const float* g,
 
 extern "C" const char* gdn_last_error(void) { return gdn_host::g_last_error.c_str(); }
 
-extern "C" int gdn_abi_version(void) { return 100; }
+extern "C" int gdn_abi_version(void) { return 101; }

@@ -1,0 +1,85 @@
+// Internal interface between the chunked forward (gdn_chunk.hip) and the
+// chunked backward (gdn_chunk_bwd.hip): the workspace layout, sequence
+// bounds, the transposing LDS read and the forward launcher the backward
+// reuses to recompute (and save) the forward chain.
+#pragma once
+
+#include "gdn_common.h"
+
+namespace gdn {
+
+// Device workspace of one chunked call, per (global chunk, v-head) unless
+// stated.  The backward-only buffers are NULL in a plain forward call.
+struct ChunkWs {
+  int32_t* off;     // [N+1] first global chunk of each sequence
+  float* gate;      // [NC][Hv][64]: G_i, the chunk-local cumulative log-decay
+  u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
+  u16x8* pfrag;     // [NC][Hv][4][2][64]
+  uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] (use_qk_l2norm only),
+  uint16_t* kn;     // written by the prep kernel, read by the chain
+  // backward only
+  float* tmat;      // [NC][Hv][64][64] T = (I + A)^-1 (fp32, row-major, upper part 0)
+  u16x8* ttfrag;    // [NC][Hv][4][2][2][64] A-operand fragments of Tb^T (hi, lo)
+  u16x8* ptfrag;    // [NC][Hv][4][2][64]    A-operand fragments of P^T
+  uint16_t* hs;     // [NC][Hv][K][V] bf16: state at the start of every chunk
+  uint16_t* dl;     // [B*T][Hv][V]   bf16: d = vnew, the per-token delta
+};
+
+__device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int total,
+                                           int& s, int& e) {
+  if (cu) {
+    s = min(max(cu[n], 0), total);
+    e = min(max(cu[n + 1], s), total);
+  } else {
+    s = n * T;
+    e = s + T;
+  }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// (i % 4) of the 4 x 16-bit words read by lanes 4m + i / 4, m = 0..3.  A
+// group reading 4 rows x 16 columns of a row-major tile thus gets the tile's
+// columns: lane i holds column i of the 4 rows.
+__device__ __forceinline__ u16x4 lds_tr16(const uint16_t* p) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (s16x4 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(u16x4, r);
+}
+
+// A-operand fragment of X^T (equivalently the B-operand fragment of X) from
+// a row-major bf16 tile X in LDS with row stride ld: lane (r16, grp) gets
+// X[k0 + 8 grp + i][m0 + r16], i = 0..7.  m0 % 4 == 0 and ld % 4 == 0.
+__device__ __forceinline__ u16x8 lds_colfrag(const uint16_t* X, int ld, int k0, int m0,
+                                             int lane) {
+  const int r16 = lane % 16, grp = lane / 16;
+  const int m4 = r16 >> 2, q4 = r16 & 3;
+  const u16x4 lo = lds_tr16(X + (k0 + 8 * grp + m4) * ld + m0 + 4 * q4);
+  const u16x4 hi = lds_tr16(X + (k0 + 8 * grp + 4 + m4) * ld + m0 + 4 * q4);
+  return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Workspace plan (byte offsets into the caller's buffer).
+struct WsPlan {
+  size_t off, gate, tfrag, pfrag, qn, kn, total;
+  // backward only (0 when not planned)
+  size_t tmat, ttfrag, ptfrag, hs, dl, dse, dd;
+  long long ncmax;
+};
+
+WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, bool l2,
+               bool bwd);
+
+// Enqueue the chunk table, the prep and the forward chain.  With `bwd` the
+// prep also writes tmat / ttfrag / ptfrag and the chain saves hs / dl
+// instead of writing o (o and ht are then ignored).
+void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                      const float* beta, const float* h0, float* ht, uint16_t* o,
+                      const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N,
+                      float scale, bool l2, bool bwd, const WsPlan& p, unsigned char* wsb,
+                      hipStream_t st);
+
+ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb);
+
+}  // namespace gdn

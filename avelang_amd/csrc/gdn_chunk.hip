@@ -28,30 +28,9 @@
 // Precision: the three products that feed the state (K S, Tb Y, K^T U) use
 // hi+lo bf16 splits of their fp32 operand(s); Q S and P vnew (output only)
 // use single bf16.
-#include "gdn_common.h"
+#include "gdn_chunk.h"
 
 namespace gdn {
-
-// ---------------------------------------------------------------- layout --
-struct ChunkWs {
-  int32_t* off;     // [N+1] first global chunk of each sequence
-  float* gate;      // [NC][Hv][64]: G_i, the chunk-local cumulative log-decay
-  u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
-  u16x8* pfrag;     // [NC][Hv][4][2][64]
-  uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] (use_qk_l2norm only),
-  uint16_t* kn;     // written by the prep kernel, read by the chain
-};
-
-__device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int total,
-                                           int& s, int& e) {
-  if (cu) {
-    s = min(max(cu[n], 0), total);
-    e = min(max(cu[n + 1], s), total);
-  } else {
-    s = n * T;
-    e = s + T;
-  }
-}
 
 // -------------------------------------------------------- chunk table ----
 __global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restrict__ cu,
@@ -98,7 +77,9 @@ __device__ __forceinline__ void scale_frags(u16x8 (&f)[KB], float r) {
 }
 
 // One workgroup per (chunk, v-head).  Wave w owns chunk rows 16w..16w+15.
-template <int K>
+// BWD (the backward's recomputation) also writes T itself and the A-operand
+// fragments of Tb^T and P^T for the reverse chain.
+template <int K, bool BWD>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ g, const float* __restrict__ beta,
@@ -118,6 +99,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   __shared__ __attribute__((aligned(16))) float AdT[4][16][16];
   __shared__ __attribute__((aligned(16))) float Bs[64];
   __shared__ __attribute__((aligned(16))) float Gs[64];
+  // P (bf16, row-major) for the P^T fragments (backward only)
+  __shared__ __attribute__((aligned(16))) uint16_t Ps[BWD ? 64 : 1][72];
 
   const int ci = blockIdx.x;
   const int h = blockIdx.y;
@@ -267,6 +250,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       pv[r] = f2bf(scale * pt[r] * gam);
     }
     if (tc < w) *reinterpret_cast<f32x4*>(&Ab[w * (w - 1) / 2 + tc][r16][4 * grp]) = av;
+    if constexpr (BWD) *reinterpret_cast<u16x4*>(&Ps[i][16 * tc + 4 * grp]) = pv;
     // P fragment slot: k-block tc/2, fragment lane r16 + 16 (2 (tc%2) + grp/2),
     // elements 4 (grp%2) .. +3
     // (k-block 1 of row tiles 0 and 1 is zero and never read: not stored)
@@ -353,6 +337,38 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + lane] = th;
     ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
   }
+  if constexpr (BWD) {
+    // Tb^T fragments, row tile w: Tb^T[m][kk] = T[kk][m] beta_m (kk >= m)
+    const int m = 16 * w + r16;
+    const float bm = Bs[m];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      u16x8 th, tl;
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii) {
+        const int kk = 32 * b + 8 * grp + ii;
+        const float x = kk >= m ? Tm[kk * kLdA + m] * bm : 0.f;
+        uint16_t xh, xl;
+        split_bf(x, xh, xl);
+        th[ii] = xh;
+        tl[ii] = xl;
+      }
+      ws.ttfrag[((base * 2 + b) * 2 + 0) * 64 + lane] = th;
+      ws.ttfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
+      // P^T fragments: P^T[m][kk] = P[kk][m]
+      ws.ptfrag[(base * 2 + b) * 64 + lane] = lds_colfrag(&Ps[0][0], 72, 32 * b, 16 * w, lane);
+    }
+    // T itself, row-major fp32 with the (unwritten) upper blocks as zero
+    float* tdst = ws.tmat + ((size_t)ci * Hv + h) * 64 * 64;
+    const int tr = tid / 4, tc0 = 16 * (tid % 4);
+#pragma unroll
+    for (int c4 = 0; c4 < 16; c4 += 4) {
+      f32x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = (tc0 + c4 + r <= tr) ? Tm[tr * kLdA + tc0 + c4 + r] : 0.f;
+      *reinterpret_cast<f32x4*>(tdst + tr * 64 + tc0 + c4) = x;
+    }
+  }
 }
 
 // --------------------------------------------------------- chain (K2) ----
@@ -360,18 +376,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 // step ahead in parts so the vector-memory queue never stalls a wave for
 // long: A (K rows) before the K S products, B (Tb, P fragments) and Q rows
 // after the first barrier, C (V column slice, G) after the second.
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
-// (i % 4) of the 4 x 16-bit words read by lanes 4m + i / 4, m = 0..3.  A
-// group reading 4 rows x 16 columns of a row-major tile thus gets the tile's
-// columns: lane i holds column i of the 4 rows.
-__device__ __forceinline__ u16x4 lds_tr16(const uint16_t* p) {
-  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (s16x4 __attribute__((address_space(3)))*)(p));
-  return __builtin_bit_cast(u16x4, r);
-}
-
 template <int K>
 struct ChainIn {
   static constexpr int KB = K / 32;
@@ -463,7 +467,9 @@ __device__ __forceinline__ void chain_load_c(ChainIn<K>& in, const ChainCtx& c, 
   in.G = c.ws.gate[((size_t)ci * c.Hv + c.h) * 64 + c.lane];
 }
 
-template <int K>
+// SAVE (the backward's recomputation): store the state at every chunk start
+// (ws.hs) and the per-token delta (ws.dl) instead of writing o.
+template <int K, bool SAVE>
 __global__ __launch_bounds__(256) void chunk_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
@@ -542,6 +548,15 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   auto step = [&](const ChainIn<K>& cur, ChainIn<K>& nxt, int ci, int cn) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
+    if constexpr (SAVE) {
+      uint16_t* hd = ws.hs + ((size_t)ci * Hv + h) * K * V + 16 * vt + r16;
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt) {
+        const u16x4 s4 = f2bf4(Sr[tt]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hd[(size_t)(w * 16 * RT + 16 * tt + 4 * grp + r) * V] = s4[r];
+      }
+    }
     chain_load_a<K>(nxt, ctx, cn);
     // gate factors of this wave's rows 16w + 4grp + r: e^G, e^(G_last - G),
     // and e^G_last (row L - 1), from the one G value each lane loaded
@@ -638,7 +653,18 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       const u16x4 vb = f2bf4(vn);
       *reinterpret_cast<u16x4*>(&UsT[0][r16][16 * w + 4 * grp]) = uh;
       *reinterpret_cast<u16x4*>(&UsT[1][r16][16 * w + 4 * grp]) = ul;
-      *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
+      if constexpr (SAVE) {
+        // delta rows 16w + 4grp + r of this chunk (rows >= L dropped by the
+        // buffer range)
+        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+            ws.dl + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          __builtin_amdgcn_raw_buffer_store_b16(
+              vb[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
+      } else {
+        *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
+      }
     }
     __syncthreads();
     chain_load_c<K>(nxt, ctx, cn);
@@ -663,7 +689,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     }
     // o^T = scale e^G (Q S)^T + vnew^T P^T: lane holds row 16w + r16,
     // columns 16 vt + 4 grp .. + 3
-    {
+    if constexpr (!SAVE) {
       const u16x8 v0 = *reinterpret_cast<const u16x8*>(&VnT[r16][8 * grp]);
       const u16x8 v1 = *reinterpret_cast<const u16x8*>(&VnT[r16][32 + 8 * grp]);
       const f32x4 oa = mfma16(v0, cur.pf[0], zero4());
@@ -718,59 +744,98 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 // ------------------------------------------------------------- host ----
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-struct WsPlan {
-  size_t off, gate, tfrag, pfrag, qn, kn, total;
-  long long ncmax;
-};
-
-static WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int N, bool has_cu, bool l2) {
+WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, bool l2,
+               bool bwd) {
   WsPlan p{};
   const long long total = (long long)B * T;
   p.ncmax = has_cu ? (total + 63LL * N) / 64 : (long long)B * ((T + 63) / 64);
+  const size_t nch = (size_t)p.ncmax * Hv;   // (chunk, v-head) pairs
   size_t at = 0;
-  p.off = at;
-  at = align256(at + (size_t)(N + 1) * 4);
-  p.gate = at;
-  at = align256(at + (size_t)p.ncmax * Hv * 64 * 4);
-  p.tfrag = at;
-  at = align256(at + (size_t)p.ncmax * Hv * 4 * 2 * 2 * 64 * 16);
-  p.pfrag = at;
-  at = align256(at + (size_t)p.ncmax * Hv * 4 * 2 * 64 * 16);
+  auto take = [&](size_t bytes) {
+    const size_t here = at;
+    at = align256(at + bytes);
+    return here;
+  };
+  p.off = take((size_t)(N + 1) * 4);
+  p.gate = take(nch * 64 * 4);
+  p.tfrag = take(nch * 4 * 2 * 2 * 64 * 16);
+  p.pfrag = take(nch * 4 * 2 * 64 * 16);
   p.qn = p.kn = at;
   if (l2) {
-    p.qn = at;
-    at = align256(at + (size_t)total * Hqk * K * 2);
-    p.kn = at;
-    at = align256(at + (size_t)total * Hqk * K * 2);
+    p.qn = take((size_t)total * Hqk * K * 2);
+    p.kn = take((size_t)total * Hqk * K * 2);
+  }
+  if (bwd) {
+    p.tmat = take(nch * 64 * 64 * 4);
+    p.ttfrag = take(nch * 4 * 2 * 2 * 64 * 16);
+    p.ptfrag = take(nch * 4 * 2 * 64 * 16);
+    p.hs = take(nch * K * V * 2);
+    p.dse = take(nch * K * V * 2);
+    p.dl = take((size_t)total * Hv * V * 2);
+    p.dd = take((size_t)total * Hv * V * 2);
   }
   p.total = at;
   return p;
 }
 
-template <int K>
-static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                         const float* g, const float* beta, const float* h0, float* ht,
-                         uint16_t* o, const int32_t* cu, int B, int T, int Hqk, int Hv, int V,
-                         int N, float scale, bool l2, const WsPlan& p, unsigned char* wsb,
-                         hipStream_t st) {
-  ChunkWs ws;
+ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb) {
+  ChunkWs ws{};
   ws.off = reinterpret_cast<int32_t*>(wsb + p.off);
   ws.gate = reinterpret_cast<float*>(wsb + p.gate);
   ws.tfrag = reinterpret_cast<u16x8*>(wsb + p.tfrag);
   ws.pfrag = reinterpret_cast<u16x8*>(wsb + p.pfrag);
   ws.qn = reinterpret_cast<uint16_t*>(wsb + p.qn);
   ws.kn = reinterpret_cast<uint16_t*>(wsb + p.kn);
+  if (p.hs) {
+    ws.tmat = reinterpret_cast<float*>(wsb + p.tmat);
+    ws.ttfrag = reinterpret_cast<u16x8*>(wsb + p.ttfrag);
+    ws.ptfrag = reinterpret_cast<u16x8*>(wsb + p.ptfrag);
+    ws.hs = reinterpret_cast<uint16_t*>(wsb + p.hs);
+    ws.dl = reinterpret_cast<uint16_t*>(wsb + p.dl);
+  }
+  return ws;
+}
+
+template <int K, bool BWD>
+static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const float* g, const float* beta, const float* h0, float* ht,
+                         uint16_t* o, const int32_t* cu, int B, int T, int Hqk, int Hv, int V,
+                         int N, float scale, bool l2, const WsPlan& p, unsigned char* wsb,
+                         hipStream_t st) {
+  const ChunkWs ws = ws_pointers(p, wsb);
   const int total = B * T;
   if (cu)
     hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, st, cu, N, T, total,
                        (int)p.ncmax, ws.off);
   if (p.ncmax > 0)
-    hipLaunchKernelGGL((chunk_prep_kernel<K>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0, st, q,
-                       k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
+    hipLaunchKernelGGL((chunk_prep_kernel<K, BWD>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0,
+                       st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised
-  hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st,
-                     l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V,
-                     scale, ws);
+  hipLaunchKernelGGL((chunk_chain_kernel<K, BWD>), dim3(N * Hv * (V / 16)), dim3(256), 0, st,
+                     l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, BWD ? nullptr : ht,
+                     BWD ? nullptr : o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+}
+
+void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                      const float* beta, const float* h0, float* ht, uint16_t* o,
+                      const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N,
+                      float scale, bool l2, bool bwd, const WsPlan& p, unsigned char* wsb,
+                      hipStream_t st) {
+  if (K == 128) {
+    if (bwd)
+      launch_chunk<128, true>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2,
+                              p, wsb, st);
+    else
+      launch_chunk<128, false>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2,
+                               p, wsb, st);
+  } else {
+    if (bwd)
+      launch_chunk<64, true>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2, p,
+                             wsb, st);
+    else
+      launch_chunk<64, false>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2,
+                              p, wsb, st);
+  }
 }
 
 }  // namespace gdn
@@ -783,9 +848,9 @@ int validate_common(const void* q, const void* k, const void* v, const float* g,
 
 extern "C" size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
                                             int N, int has_cu_seqlens, int use_qk_l2norm) {
-  (void)V;
-  if (B < 0 || T < 0 || Hqk <= 0 || Hv <= 0 || N < 0 || K <= 0) return 0;
-  return gdn::plan_ws(B, T, Hqk, Hv, K, N, has_cu_seqlens != 0, use_qk_l2norm != 0).total;
+  if (B < 0 || T < 0 || Hqk <= 0 || Hv <= 0 || N < 0 || K <= 0 || V <= 0) return 0;
+  return gdn::plan_ws(B, T, Hqk, Hv, K, V, N, has_cu_seqlens != 0, use_qk_l2norm != 0, false)
+      .total;
 }
 
 extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
@@ -797,25 +862,18 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
                                      K, V, N);
   if (rc) return rc;
   if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
-  const gdn::WsPlan p =
-      gdn::plan_ws(B, T, Hqk, Hv, K, N, cu_seqlens != nullptr, use_qk_l2norm != 0);
+  const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
+                                     use_qk_l2norm != 0, false);
   if (!workspace || workspace_bytes < p.total)
     return gdn_host::fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace needs " +
                                                  std::to_string(p.total) + " bytes, got " +
                                                  std::to_string(workspace_bytes));
   if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
     return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_fwd: problem too large");
-  auto* qq = static_cast<const uint16_t*>(q);
-  auto* kk = static_cast<const uint16_t*>(k);
-  auto* vv = static_cast<const uint16_t*>(v);
-  auto* oo = static_cast<uint16_t*>(o);
-  auto* wsb = static_cast<unsigned char*>(workspace);
-  auto st = static_cast<hipStream_t>(stream);
-  if (K == 128)
-    gdn::launch_chunk<128>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, Hv, V, N,
-                           scale, use_qk_l2norm != 0, p, wsb, st);
-  else
-    gdn::launch_chunk<64>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, Hv, V, N,
-                          scale, use_qk_l2norm != 0, p, wsb, st);
+  gdn::launch_chunk_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                        static_cast<const uint16_t*>(v), g, beta, h0, ht,
+                        static_cast<uint16_t*>(o), cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
+                        use_qk_l2norm != 0, false, p, static_cast<unsigned char*>(workspace),
+                        static_cast<hipStream_t>(stream));
   return gdn_host::check_launch("gdn_chunk_fwd");
 }

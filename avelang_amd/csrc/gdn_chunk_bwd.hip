@@ -1,0 +1,892 @@
+// Chunked gated-delta-rule BACKWARD for gfx950 (chunk = 64 tokens).
+//
+// The reference repository has no gated delta rule (forward or backward);
+// the operator is FLA's chunk_gated_delta_rule, whose forward semantics are
+// transformers modeling_qwen3_next.py:374-453.  The gradient below is
+// reverse-mode differentiation of the chunked forward of gdn_chunk.hip.
+//
+// Per chunk c (rows i, j in [0, 64), c' = scale, S = state at the chunk's
+// start, dS' = dL/d(state at its end) from later chunks):
+//   d     = Tb (V - e^G * (K S))                 (forward: the per-token delta)
+//   dd    = P^T dO + e^(G_L - G) * (K dS')       (dL/dd; P carries c')
+//   Z     = Tb^T dd
+//   dS    = e^G_L dS' - K^T (e^G * Z) + Q^T (c' e^G * dO)
+// and every gradient of the chunk is local given S, dS', d and dd.
+//
+// Launches (after the forward's chunk table + prep in backward mode, which
+// also writes T, Tb^T and P^T, and the forward chain in save mode, which
+// stores S at every chunk start and d):
+//   chunk_rev_kernel    one workgroup per (sequence, v-head, 16-column V
+//                       tile), reverse over the sequence's chunks; dS' in
+//                       VGPRs (fp32), every product a 16x16x32 bf16 MFMA with
+//                       hi+lo splits where it feeds dS (as the forward chain);
+//                       stores dS' of every chunk and dd (bf16) and dh0
+//   chunk_grad_kernel   one workgroup per (chunk, qk-head), fully parallel:
+//                       the local gradients of the group's v-heads, dq / dk
+//                       summed over the group in registers
+#include "gdn_chunk.h"
+
+namespace gdn {
+
+struct BwdWs {
+  ChunkWs f;              // forward workspace (gate, fragments, T, hs, dl, ...)
+  uint16_t* dse;          // [NC][Hv][K][V] bf16: dL/d(end state) of every chunk
+  uint16_t* dd;           // [B*T][Hv][V]   bf16: dL/dd
+};
+
+// ------------------------------------------------------ reverse chain ----
+template <int K>
+struct RevIn {
+  static constexpr int KB = K / 32;
+  u16x8 kf[KB], qf[KB];   // K / Q rows 16w + r16 (A operand of K dS'; staged for K^T, Q^T)
+  u16x8 tf[2][2];         // Tb^T rows [k-block][hi, lo]
+  u16x8 pf[2];            // P^T rows [k-block]
+  u16x8 dof[2];           // dO[32 kb + 8 grp + i][16 vt + r16], i = 0..7 (B operand)
+  float G;                // G of row `lane`
+};
+
+struct RevCtx {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* dO;
+  BwdWs ws;
+  int s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane;
+  int kq_off;     // row 16w + r16, columns 8grp.. of a K / Q row (bytes)
+};
+
+template <int K>
+__device__ __forceinline__ void rev_load_a(RevIn<K>& in, const RevCtx& c, int ci) {
+  const int t0 = c.s + (ci - c.c_begin) * kChunk;
+  const int L = min(kChunk, c.e - t0);
+  const size_t row0 = (size_t)t0 * c.Hqk + c.hq;
+  const int bytes = L * c.Hqk * K * 2;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(c.k + row0 * K), 0, bytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(c.q + row0 * K), 0, bytes, kBufferFlags);
+#pragma unroll
+  for (int b = 0; b < RevIn<K>::KB; ++b) {
+    in.kf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, c.kq_off + 64 * b, 0, 0));
+    in.qf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, c.kq_off + 64 * b, 0, 0));
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void rev_load_b(RevIn<K>& in, const RevCtx& c, int ci) {
+  const size_t base = ((size_t)ci * c.Hv + c.h) * 4 + c.w;
+  const u16x8* tb = c.ws.f.ttfrag + base * 256;
+  const u16x8* pb = c.ws.f.ptfrag + base * 128;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    in.tf[b][0] = tb[128 * b + c.lane];
+    in.tf[b][1] = tb[128 * b + 64 + c.lane];
+    in.pf[b] = pb[64 * b + c.lane];
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void rev_load_c(RevIn<K>& in, const RevCtx& c, int ci) {
+  const int t0 = c.s + (ci - c.c_begin) * kChunk;
+  const int L = min(kChunk, c.e - t0);
+  const int rowb = c.Hv * c.V * 2;
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(c.dO + ((size_t)t0 * c.Hv + c.h) * c.V + 16 * c.vt), 0,
+      (L - 1) * rowb + 32, kBufferFlags);
+  const int grp = c.lane / 16, r16 = c.lane % 16;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      in.dof[kb][i] = __builtin_amdgcn_raw_buffer_load_b16(
+          rd, (32 * kb + 8 * grp + i) * rowb + 2 * r16, 0, 0);
+  }
+  in.G = c.ws.f.gate[((size_t)ci * c.Hv + c.h) * 64 + c.lane];
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void chunk_rev_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ dO, const float* dht, float* dh0,
+    const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
+    float scale, BwdWs ws) {
+  constexpr int KB = K / 32;
+  constexpr int RT = K / 64;     // 16-row state tiles per wave
+  constexpr int LDS_ = K + 8;
+  constexpr int LDY = 72;
+  static_assert(KB % 2 == 0, "K dS' uses two accumulators per hi/lo part");
+  __shared__ __attribute__((aligned(16))) uint16_t DsT[2][16][LDS_];
+  __shared__ __attribute__((aligned(16))) uint16_t YsT[2][16][LDY];
+  __shared__ __attribute__((aligned(16))) uint16_t ZsT[2][16][LDY];
+  __shared__ __attribute__((aligned(16))) uint16_t Kl[64][LDS_];
+  __shared__ __attribute__((aligned(16))) uint16_t Ql[64][LDS_];
+  __shared__ __attribute__((aligned(16))) float Egw[4][64];   // wave-private e^G
+
+  const int NVT = V / 16;
+  // blockIdx -> (sequence, v-head, V tile) dealt over the XCDs as the
+  // forward chain does (a qk-head group stays on one XCD)
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  const int unit = NVT * (Hv / Hqk);
+  if (nb % (8 * unit) == 0) {
+    const int i = bid >> 3;
+    bid = ((i / unit) * 8 + (bid & 7)) * unit + i % unit;
+  } else if ((nb & 7) == 0) {
+    bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  }
+  const int vt = bid % NVT;
+  const int h = (bid / NVT) % Hv;
+  const int n = bid / NVT / Hv;
+  const int hq = h / (Hv / Hqk);
+
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const int r16 = lane % 16, grp = lane / 16;
+
+  int s, e;
+  seq_bounds(cu, n, T, total, s, e);
+  const int nct = (T + kChunk - 1) / kChunk;
+  const int c_begin = cu ? ws.f.off[n] : n * nct, c_end = cu ? ws.f.off[n + 1] : (n + 1) * nct;
+  const RevCtx ctx{q, k, dO, ws, s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane,
+                   ((16 * w + r16) * Hqk * K + 8 * grp) * 2};
+
+  // dS' slice: rows w*16*RT + 16*tt + 4*grp + r, column 16*vt + r16
+  const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
+  f32x4 Dr[RT];
+#pragma unroll
+  for (int tt = 0; tt < RT; ++tt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
+      Dr[tt][r] = dht ? dht[tile + (size_t)kd * V] : 0.f;
+    }
+  }
+  auto publish = [&]() {
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+      u16x4 hi4, lo4;
+      split_bf4(Dr[tt], hi4, lo4);
+      const int kd0 = w * 16 * RT + 16 * tt + 4 * grp;
+      *reinterpret_cast<u16x4*>(&DsT[0][r16][kd0]) = hi4;
+      *reinterpret_cast<u16x4*>(&DsT[1][r16][kd0]) = lo4;
+    }
+  };
+  publish();
+  __syncthreads();
+
+  auto step = [&](const RevIn<K>& cur, RevIn<K>& nxt, int ci, int cn) {
+    const int t0 = s + (ci - c_begin) * kChunk;
+    const int L = min(kChunk, e - t0);
+    // dS' of this chunk for the gradient kernel
+    {
+      uint16_t* dst = ws.dse + ((size_t)ci * Hv + h) * K * V + 16 * vt + r16;
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt) {
+        const u16x4 d4 = f2bf4(Dr[tt]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(size_t)(w * 16 * RT + 16 * tt + 4 * grp + r) * V] = d4[r];
+      }
+    }
+    rev_load_a<K>(nxt, ctx, cn);
+    const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.G), L - 1));
+    const float egx = __expf(cur.G), decx = __expf(GL - cur.G);
+    f32x4 eg, dec;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int src = (16 * w + 4 * grp + r) * 4;
+      eg[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(egx)));
+      dec[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(decx)));
+    }
+    const float egl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(egx), L - 1));
+    Egw[w][lane] = egx;
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = cur.kf[b];
+      *reinterpret_cast<u16x8*>(&Ql[16 * w + r16][32 * b + 8 * grp]) = cur.qf[b];
+    }
+    // X = K dS' (hi + lo)
+    f32x4 xa = zero4(), xb = zero4(), xc = zero4(), xd = zero4();
+#pragma unroll
+    for (int b = 0; b < KB; b += 2) {
+      const u16x8 sh0 = *reinterpret_cast<const u16x8*>(&DsT[0][r16][32 * b + 8 * grp]);
+      const u16x8 sl0 = *reinterpret_cast<const u16x8*>(&DsT[1][r16][32 * b + 8 * grp]);
+      const u16x8 sh1 = *reinterpret_cast<const u16x8*>(&DsT[0][r16][32 * b + 32 + 8 * grp]);
+      const u16x8 sl1 = *reinterpret_cast<const u16x8*>(&DsT[1][r16][32 * b + 32 + 8 * grp]);
+      xa = mfma16(cur.kf[b], sh0, xa);
+      xb = mfma16(cur.kf[b + 1], sh1, xb);
+      xc = mfma16(cur.kf[b], sl0, xc);
+      xd = mfma16(cur.kf[b + 1], sl1, xd);
+    }
+    // P^T dO (bf16 operands, exact products)
+    const f32x4 pd = mfma16(cur.pf[1], cur.dof[1], mfma16(cur.pf[0], cur.dof[0], zero4()));
+    {
+      const f32x4 X = (xa + xb) + (xc + xd);
+      const f32x4 y = dec * X + pd;
+      u16x4 yh, yl;
+      split_bf4(y, yh, yl);
+      *reinterpret_cast<u16x4*>(&YsT[0][r16][16 * w + 4 * grp]) = yh;
+      *reinterpret_cast<u16x4*>(&YsT[1][r16][16 * w + 4 * grp]) = yl;
+      // dd rows 16w + 4grp + r (rows >= L dropped by the buffer range)
+      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+          ws.dd + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_raw_buffer_store_b16(
+            yh[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
+    }
+    __syncthreads();
+    rev_load_b<K>(nxt, ctx, cn);
+
+    // K^T and Q^T fragments of the update (rows of this wave's state tiles)
+    u16x8 ka[RT][2], qa[RT][2];
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+      const int kd0 = w * 16 * RT + 16 * tt;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        ka[tt][b] = lds_colfrag(&Kl[0][0], LDS_, 32 * b, kd0, lane);
+        qa[tt][b] = lds_colfrag(&Ql[0][0], LDS_, 32 * b, kd0, lane);
+      }
+    }
+    // Z = Tb^T dd (three hi/lo terms)
+    {
+      f32x4 va = zero4(), vb = zero4(), vc = zero4();
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const u16x8 yh = *reinterpret_cast<const u16x8*>(&YsT[0][r16][32 * b + 8 * grp]);
+        const u16x8 yl = *reinterpret_cast<const u16x8*>(&YsT[1][r16][32 * b + 8 * grp]);
+        va = mfma16(cur.tf[b][0], yh, va);
+        vb = mfma16(cur.tf[b][0], yl, vb);
+        vc = mfma16(cur.tf[b][1], yh, vc);
+      }
+      const f32x4 z = -(eg * (va + (vb + vc)));
+      u16x4 zh, zl;
+      split_bf4(z, zh, zl);
+      *reinterpret_cast<u16x4*>(&ZsT[0][r16][16 * w + 4 * grp]) = zh;
+      *reinterpret_cast<u16x4*>(&ZsT[1][r16][16 * w + 4 * grp]) = zl;
+    }
+    // B operand of the Q^T term: c' e^G_j dO[j], j = 32 kb + 8 grp + i (hi + lo)
+    u16x8 oh[2], ol[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const f32x4 e0 = *reinterpret_cast<const f32x4*>(&Egw[w][32 * kb + 8 * grp]);
+      const f32x4 e1 = *reinterpret_cast<const f32x4*>(&Egw[w][32 * kb + 8 * grp + 4]);
+      f32x4 x0, x1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x0[i] = scale * e0[i] * bf2f(cur.dof[kb][i]);
+        x1[i] = scale * e1[i] * bf2f(cur.dof[kb][4 + i]);
+      }
+      u16x4 h0v, l0v, h1v, l1v;
+      split_bf4(x0, h0v, l0v);
+      split_bf4(x1, h1v, l1v);
+      oh[kb] = u16x8{h0v[0], h0v[1], h0v[2], h0v[3], h1v[0], h1v[1], h1v[2], h1v[3]};
+      ol[kb] = u16x8{l0v[0], l0v[1], l0v[2], l0v[3], l1v[0], l1v[1], l1v[2], l1v[3]};
+    }
+    __syncthreads();
+    rev_load_c<K>(nxt, ctx, cn);
+
+    // dS = e^G_L dS' + K^T (-e^G Z) + Q^T (c' e^G dO)
+    {
+      u16x8 zh[2], zl[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        zh[b] = *reinterpret_cast<const u16x8*>(&ZsT[0][r16][32 * b + 8 * grp]);
+        zl[b] = *reinterpret_cast<const u16x8*>(&ZsT[1][r16][32 * b + 8 * grp]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt) {
+        f32x4 a0 = Dr[tt] * egl, a1 = zero4(), a2 = zero4(), a3 = zero4();
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          a0 = mfma16(ka[tt][b], zh[b], a0);
+          a1 = mfma16(ka[tt][b], zl[b], a1);
+          a2 = mfma16(qa[tt][b], oh[b], a2);
+          a3 = mfma16(qa[tt][b], ol[b], a3);
+        }
+        Dr[tt] = (a0 + a1) + (a2 + a3);
+      }
+    }
+    publish();
+    __syncthreads();
+  };
+
+  RevIn<K> bufA, bufB;
+  if (c_begin < c_end) {
+    rev_load_a<K>(bufA, ctx, c_end - 1);
+    rev_load_b<K>(bufA, ctx, c_end - 1);
+    rev_load_c<K>(bufA, ctx, c_end - 1);
+  }
+  for (int ci = c_end - 1; ci >= c_begin; ci -= 2) {
+    step(bufA, bufB, ci, max(ci - 1, c_begin));
+    if (ci - 1 < c_begin) break;
+    step(bufB, bufA, ci - 1, max(ci - 2, c_begin));
+  }
+
+  if (dh0) {
+#pragma unroll
+    for (int tt = 0; tt < RT; ++tt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
+        dh0[tile + (size_t)kd * V] = Dr[tt][r];
+      }
+    }
+  }
+}
+
+}  // namespace gdn
+
+namespace gdn {
+
+// --------------------------------------------------- gradient kernel ----
+// One workgroup per (chunk, qk-head); wave w owns chunk rows 16w..16w+15 of
+// every [64 x *] result.  "OL" = the MFMA output layout: lane (r16, grp)
+// holds rows 16w + 4grp + r (r = 0..3) of column 16ct + r16.
+//
+// Local gradients of one (chunk, v-head) given S (chunk start state), dS'
+// (gradient into its end state), d and dd (all bf16 from the chains):
+//   R1 = dO S^T, R2 = dd S^T, dKt = d dS'^T              (streamed, no LDS)
+//   dPt = lower_incl(c' dO d^T),  dT = dd (bV)^T - R2 (b e^G K)^T
+//   dA = strict_lower(-T^T dT T^T)                       (fp32 MFMA)
+//   M = dA * b_i Gam,  MP = dPt * Gam
+//   dq = c' e^G R1 + MP K
+//   dk = e^(G_L - G) dKt + b e^G (T^T dW) + M K + M^T K + MP^T Q,  dW = -R2
+//   dv = b (T^T dd)
+//   dbeta = V . (T^T dd) + e^G K . (T^T dW) + rowsum(dA KK Gam)
+//   dG = c' e^G Q.R1 - rho + b e^G K.(T^T dW) + rowsum(X) - colsum(X)
+//        (+ e^G_L <S, dS'> + sum(rho) on the last row),
+//   X = (b_i dA KK + dPt QK) Gam,  rho_j = e^(G_L - G_j) K_j . dKt_j
+//   dg = reverse cumsum of dG within the chunk.
+// (c' is folded into dO: dPt and R1 use c' dO.)
+template <int K, int V>
+__global__ __launch_bounds__(256) void chunk_grad_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ qraw, const uint16_t* __restrict__ kraw,
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ dO,
+    const float* __restrict__ beta, const int32_t* __restrict__ cu, int N, int T, int total,
+    int Hqk, int Hv, float scale, int l2norm, BwdWs ws, uint16_t* __restrict__ dq,
+    uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, float* __restrict__ dg,
+    float* __restrict__ dbeta) {
+  constexpr int KT = K / 16, VT = V / 16, KB = K / 32, VB = V / 32;
+  constexpr int LK = K + 8, LV = V + 8, LT = 68, LC = 72;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[64][LK];
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[64][LK];
+  __shared__ __attribute__((aligned(16))) float T32[64][LT];
+  __shared__ __attribute__((aligned(16))) float X32[64][LT];
+  __shared__ __attribute__((aligned(16))) uint16_t Tb16[64][LC];
+  // dd rows and R2 (bf16) for the T^T products; reused for M and MP after
+  constexpr int kRegA = 64 * LV * 2, kRegB = 64 * LK * 2;
+  static_assert(kRegA >= 64 * LC * 2 && kRegB >= 64 * LC * 2, "M / MP alias dd / R2");
+  __shared__ __attribute__((aligned(16))) unsigned char regA[kRegA];
+  __shared__ __attribute__((aligned(16))) unsigned char regB[kRegB];
+  uint16_t (*dds)[LV] = reinterpret_cast<uint16_t (*)[LV]>(regA);
+  uint16_t (*R2s)[LK] = reinterpret_cast<uint16_t (*)[LK]>(regB);
+  uint16_t (*Ms)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regB);
+  uint16_t (*MPs)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regA);
+  __shared__ __attribute__((aligned(16))) float Gs[64];
+  __shared__ __attribute__((aligned(16))) float Bs[64];
+  __shared__ __attribute__((aligned(16))) float Cs[64];     // column sums of X
+  __shared__ __attribute__((aligned(16))) float Ds[64];     // dG per row
+  __shared__ float Red[4];
+
+  const int ci = blockIdx.x;
+  const int hq = blockIdx.y;
+  int n, cfirst;
+  if (cu) {
+    const int32_t* off = ws.f.off;
+    if (ci >= off[N]) return;
+    int lo = 0, hi = N;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (off[mid] <= ci) lo = mid; else hi = mid;
+    }
+    n = lo;
+    cfirst = off[n];
+  } else {
+    const int nct = (T + kChunk - 1) / kChunk;
+    n = ci / nct;
+    cfirst = n * nct;
+  }
+  int s, e;
+  seq_bounds(cu, n, T, total, s, e);
+  const int t0 = s + (ci - cfirst) * kChunk;
+  const int L = min(kChunk, e - t0);
+  const int Gn = Hv / Hqk;
+
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const int r16 = lane % 16, grp = lane / 16;
+  const int rowA = 16 * w + r16;          // A-fragment row of this lane
+  const int row0 = 16 * w + 4 * grp;      // first OL row of this lane
+
+  // K / Q rows of the chunk (rows >= L read as zero)
+  const int qkbytes = L * Hqk * K * 2;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(k + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(q + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
+  for (int idx = tid; idx < 64 * K / 8; idx += 256) {
+    const int r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
+    const int off = (r * Hqk * K + c8) * 2;
+    *reinterpret_cast<u16x8*>(&Ks[r][c8]) =
+        __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+    *reinterpret_cast<u16x8*>(&Qs[r][c8]) =
+        __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+  }
+  __syncthreads();
+
+  // K K^T and Q K^T in OL (shared by the group's v-heads)
+  f32x4 kk[4], qk[4];
+  {
+    u16x8 ka[KB], qa[KB];
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      ka[b] = *reinterpret_cast<const u16x8*>(&Ks[rowA][32 * b + 8 * grp]);
+      qa[b] = *reinterpret_cast<const u16x8*>(&Qs[rowA][32 * b + 8 * grp]);
+    }
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      kk[ct] = zero4();
+      qk[ct] = zero4();
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        const u16x8 kb = *reinterpret_cast<const u16x8*>(&Ks[16 * ct + r16][32 * b + 8 * grp]);
+        kk[ct] = mfma16(ka[b], kb, kk[ct]);
+        qk[ct] = mfma16(qa[b], kb, qk[ct]);
+      }
+    }
+  }
+
+  f32x4 dQa[KT], dKa[KT];
+#pragma unroll
+  for (int ct = 0; ct < KT; ++ct) {
+    dQa[ct] = zero4();
+    dKa[ct] = zero4();
+  }
+
+  const int vbytes = L * Hv * V * 2;
+  for (int gi = 0; gi < Gn; ++gi) {
+    const int h = hq * Gn + gi;
+    const size_t ch = (size_t)ci * Hv + h;
+    // ---- per-v-head operands into LDS: T (fp32 + bf16), G, beta, dd rows
+    {
+      const float* tsrc = ws.f.tmat + ch * 64 * 64;
+      for (int idx = tid; idx < 64 * 16; idx += 256) {
+        const int r = idx / 16, c4 = 4 * (idx % 16);
+        const f32x4 x = *reinterpret_cast<const f32x4*>(tsrc + r * 64 + c4);
+        *reinterpret_cast<f32x4*>(&T32[r][c4]) = x;
+        *reinterpret_cast<u16x4*>(&Tb16[r][c4]) = f2bf4(x);
+      }
+      if (tid < 64) {
+        Gs[tid] = ws.f.gate[ch * 64 + tid];
+        Bs[tid] = tid < L ? beta[(size_t)(t0 + tid) * Hv + h] : 0.f;
+      }
+    }
+    const __amdgpu_buffer_rsrc_t rdd = __builtin_amdgcn_make_buffer_rsrc(
+        ws.dd + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
+        ws.f.dl + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
+    for (int idx = tid; idx < 64 * V / 8; idx += 256) {
+      const int r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
+      *reinterpret_cast<u16x8*>(&dds[r][c8]) = __builtin_bit_cast(
+          u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, (r * Hv * V + c8) * 2, 0, 0));
+    }
+    // A fragments (rows rowA): dO, dd, d
+    u16x8 aO[VB], aD[VB], aL[VB];
+#pragma unroll
+    for (int b = 0; b < VB; ++b) {
+      const int off = (rowA * Hv * V + 32 * b + 8 * grp) * 2;
+      aO[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
+      aD[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, off, 0, 0));
+      aL[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
+    }
+    __syncthreads();
+
+    // row factors of this lane's OL rows
+    const float GL = Gs[L - 1];
+    f32x4 eg, dec, bt;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      eg[r] = __expf(Gs[row0 + r]);
+      dec[r] = __expf(GL - Gs[row0 + r]);
+      bt[r] = Bs[row0 + r];
+    }
+    f32x4 qr1 = zero4(), rho = zero4(), ktw = zero4(), vtu = zero4();
+
+    // ---- streamed products against S and dS' (rows of [K][V], bf16)
+    const uint16_t* Sg = ws.f.hs + ch * K * V;
+    const uint16_t* Eg = ws.dse + ch * K * V;
+    float sde = 0.f;   // partial <S, dS'>
+#pragma unroll
+    for (int ct = 0; ct < KT; ++ct) {
+      f32x4 r1 = zero4(), r2 = zero4(), dkt = zero4();
+#pragma unroll
+      for (int b = 0; b < VB; ++b) {
+        const size_t boff = (size_t)(16 * ct + r16) * V + 32 * b + 8 * grp;
+        const u16x8 sb = *reinterpret_cast<const u16x8*>(Sg + boff);
+        const u16x8 eb = *reinterpret_cast<const u16x8*>(Eg + boff);
+        r1 = mfma16(aO[b], sb, r1);
+        r2 = mfma16(aD[b], sb, r2);
+        dkt = mfma16(aL[b], eb, dkt);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sde += bf2f(sb[i]) * bf2f(eb[i]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float qv = bf2f(Qs[row0 + r][16 * ct + r16]);
+        const float kv = bf2f(Ks[row0 + r][16 * ct + r16]);
+        const float a = scale * r1[r];
+        dQa[ct][r] += eg[r] * a;
+        qr1[r] += qv * a;
+        const float d2 = dec[r] * dkt[r];
+        dKa[ct][r] += d2;
+        rho[r] += kv * d2;
+        R2s[row0 + r][16 * ct + r16] = f2bf(r2[r]);
+      }
+    }
+    // dPt = c' dO d^T and dd V^T (C x C, OL)
+    f32x4 dpt[4], ddv[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      dpt[ct] = zero4();
+      ddv[ct] = zero4();
+#pragma unroll
+      for (int b = 0; b < VB; ++b) {
+        const int off = ((16 * ct + r16) * Hv * V + 32 * b + 8 * grp) * 2;
+        const u16x8 lb = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
+        const u16x8 vb = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+        dpt[ct] = mfma16(aO[b], lb, dpt[ct]);
+        ddv[ct] = mfma16(aD[b], vb, ddv[ct]);
+      }
+    }
+    __syncthreads();   // R2s complete
+
+    // ---- dT = dd (bV)^T - R2 (b e^G K)^T  -> X32 (fp32)
+    {
+      u16x8 a2[KB];
+#pragma unroll
+      for (int b = 0; b < KB; ++b) a2[b] = *reinterpret_cast<const u16x8*>(&R2s[rowA][32 * b + 8 * grp]);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        f32x4 t2 = zero4();
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+          t2 = mfma16(a2[b], *reinterpret_cast<const u16x8*>(&Ks[16 * ct + r16][32 * b + 8 * grp]), t2);
+        const int j = 16 * ct + r16;
+        const float bj = Bs[j], bgj = bj * __expf(Gs[j]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) X32[row0 + r][j] = ddv[ct][r] * bj - t2[r] * bgj;
+      }
+    }
+    // ---- T^T dd (-> dv, dbeta) and T^T dW = -T^T R2 (-> dk, dbeta, dG)
+    {
+      u16x8 ta[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) ta[b] = lds_colfrag(&Tb16[0][0], LC, 32 * b, 16 * w, lane);
+      const __amdgpu_buffer_rsrc_t rdv = __builtin_amdgcn_make_buffer_rsrc(
+          dv + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+#pragma unroll
+      for (int ct = 0; ct < VT; ++ct) {
+        f32x4 tu = zero4();
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          tu = mfma16(ta[b], lds_colfrag(&dds[0][0], LV, 32 * b, 16 * ct, lane), tu);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float vv = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rv, ((row0 + r) * Hv * V + 16 * ct + r16) * 2, 0, 0));
+          vtu[r] += vv * tu[r];
+          __builtin_amdgcn_raw_buffer_store_b16(f2bf(bt[r] * tu[r]), rdv,
+                                                ((row0 + r) * Hv * V + 16 * ct + r16) * 2, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < KT; ++ct) {
+        f32x4 tw = zero4();
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          tw = mfma16(ta[b], lds_colfrag(&R2s[0][0], LK, 32 * b, 16 * ct, lane), tw);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = -tw[r];   // (T^T dW)
+          dKa[ct][r] += bt[r] * eg[r] * x;
+          ktw[r] += bf2f(Ks[row0 + r][16 * ct + r16]) * x;
+        }
+      }
+    }
+    __syncthreads();   // X32 = dT complete; dd / R2 no longer needed
+
+    // ---- dA = strict_lower(-T^T (dT T^T)) on fp32 MFMA (T lower triangular)
+    f32x4 m1[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      m1[ct] = zero4();
+      for (int j0 = 0; j0 < 16 * (ct + 1); j0 += 4)
+        m1[ct] = mfma4f32(X32[rowA][j0 + grp], T32[16 * ct + r16][j0 + grp], m1[ct]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) X32[row0 + r][16 * ct + r16] = m1[ct][r];
+    __syncthreads();
+    f32x4 da[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      da[ct] = zero4();
+      if (ct <= w) {
+        for (int j0 = 16 * w; j0 < 64; j0 += 4)
+          da[ct] = mfma4f32(T32[j0 + grp][rowA], X32[j0 + grp][16 * ct + r16], da[ct]);
+      }
+    }
+    __syncthreads();   // X32 (M1) reads done before X is written there
+
+    // ---- C x C elementwise: M, MP, dbeta / dG terms, X
+    f32x4 dba = zero4(), xr = zero4();
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int j = 16 * ct + r16;
+      const float Gj = Gs[j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = row0 + r;
+        const float gam = (j <= i) ? __expf(Gs[i] - Gj) : 0.f;
+        const float dA = (j < i) ? -da[ct][r] : 0.f;
+        const float dP = (j <= i) ? scale * dpt[ct][r] : 0.f;
+        Ms[i][j] = f2bf(dA * bt[r] * gam);
+        MPs[i][j] = f2bf(dP * gam);
+        dba[r] += dA * kk[ct][r] * gam;
+        const float x = (dA * bt[r] * kk[ct][r] + dP * qk[ct][r]) * gam;
+        xr[r] += x;
+        X32[i][j] = x;
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      float c = 0.f;
+      for (int i = 0; i < 64; ++i) c += X32[i][tid];
+      Cs[tid] = c;
+    }
+
+    // ---- dK += M K + M^T K + MP^T Q,  dQ += MP K
+    {
+      u16x8 am[2], amt[2], ap[2], apt[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        am[b] = *reinterpret_cast<const u16x8*>(&Ms[rowA][32 * b + 8 * grp]);
+        ap[b] = *reinterpret_cast<const u16x8*>(&MPs[rowA][32 * b + 8 * grp]);
+        amt[b] = lds_colfrag(&Ms[0][0], LC, 32 * b, 16 * w, lane);
+        apt[b] = lds_colfrag(&MPs[0][0], LC, 32 * b, 16 * w, lane);
+      }
+#pragma unroll
+      for (int ct = 0; ct < KT; ++ct) {
+        f32x4 a0 = dKa[ct], a1 = zero4(), a2 = dQa[ct];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const u16x8 kc = lds_colfrag(&Ks[0][0], LK, 32 * b, 16 * ct, lane);
+          const u16x8 qc = lds_colfrag(&Qs[0][0], LK, 32 * b, 16 * ct, lane);
+          a0 = mfma16(am[b], kc, a0);
+          a1 = mfma16(amt[b], kc, a1);
+          a1 = mfma16(apt[b], qc, a1);
+          a2 = mfma16(ap[b], kc, a2);
+        }
+        dKa[ct] = a0 + a1;
+        dQa[ct] = a2;
+      }
+    }
+
+    // ---- row reductions over the 16 lanes of a group, dG, dbeta
+#pragma unroll
+    for (int sh = 1; sh < 16; sh *= 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        qr1[r] += __shfl_xor(qr1[r], sh);
+        rho[r] += __shfl_xor(rho[r], sh);
+        ktw[r] += __shfl_xor(ktw[r], sh);
+        vtu[r] += __shfl_xor(vtu[r], sh);
+        dba[r] += __shfl_xor(dba[r], sh);
+        xr[r] += __shfl_xor(xr[r], sh);
+      }
+    }
+    // sum of rho over all rows and <S, dS'> (wave sums, then across waves)
+    float rs = (r16 == 0) ? (rho[0] + rho[1] + rho[2] + rho[3]) : 0.f;
+#pragma unroll
+    for (int sh = 16; sh < 64; sh *= 2) rs += __shfl_xor(rs, sh);
+#pragma unroll
+    for (int sh = 1; sh < 64; sh *= 2) sde += __shfl_xor(sde, sh);
+    if (lane == 0) Red[w] = rs;
+    __syncthreads();   // Cs, Red complete
+    const float rho_all = Red[0] + Red[1] + Red[2] + Red[3];
+    if (r16 == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = row0 + r;
+        float dG = eg[r] * qr1[r] - rho[r] + bt[r] * eg[r] * ktw[r] + xr[r] - Cs[i];
+        if (i == L - 1) dG += __expf(GL) * sde + rho_all;
+        Ds[i] = i < L ? dG : 0.f;
+        if (i < L)
+          dbeta[(size_t)(t0 + i) * Hv + h] = vtu[r] + eg[r] * ktw[r] + dba[r];
+      }
+    }
+    __syncthreads();
+    if (w == 0) {
+      // dg_i = sum_{m >= i} dG_m (reverse inclusive scan over the chunk)
+      float x = Ds[63 - lane];
+#pragma unroll
+      for (int d = 1; d < 64; d *= 2) {
+        const float o = __shfl_up(x, d);
+        if (lane >= d) x += o;
+      }
+      const int i = 63 - lane;
+      if (i < L) dg[(size_t)(t0 + i) * Hv + h] = x;
+    }
+    __syncthreads();   // LDS reuse by the next v-head
+  }
+
+  // ---- dq, dk: through the l2norm when the forward normalised q, k
+  const __amdgpu_buffer_rsrc_t rdq = __builtin_amdgcn_make_buffer_rsrc(
+      dq + ((size_t)t0 * Hqk + hq) * K, 0, qkbytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rdk = __builtin_amdgcn_make_buffer_rsrc(
+      dk + ((size_t)t0 * Hqk + hq) * K, 0, qkbytes, kBufferFlags);
+  if (l2norm) {
+    const __amdgpu_buffer_rsrc_t rqr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rkr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(kraw + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
+    f32x4 sq = zero4(), sk = zero4(), pq = zero4(), pk = zero4();
+    float xq[KT][4], xk[KT][4];
+#pragma unroll
+    for (int ct = 0; ct < KT; ++ct) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
+        xq[ct][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rqr, off, 0, 0));
+        xk[ct][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rkr, off, 0, 0));
+        sq[r] += xq[ct][r] * xq[ct][r];
+        sk[r] += xk[ct][r] * xk[ct][r];
+        pq[r] += xq[ct][r] * dQa[ct][r];
+        pk[r] += xk[ct][r] * dKa[ct][r];
+      }
+    }
+#pragma unroll
+    for (int sh = 1; sh < 16; sh *= 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sq[r] += __shfl_xor(sq[r], sh);
+        sk[r] += __shfl_xor(sk[r], sh);
+        pq[r] += __shfl_xor(pq[r], sh);
+        pk[r] += __shfl_xor(pk[r], sh);
+      }
+    }
+    // dx = r (dy - y (y . dy)), y = x r, r = (|x|^2 + eps)^-1/2
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float rq = rsqrtf(sq[r] + 1e-6f), rk2 = rsqrtf(sk[r] + 1e-6f);
+#pragma unroll
+      for (int ct = 0; ct < KT; ++ct) {
+        dQa[ct][r] = rq * (dQa[ct][r] - xq[ct][r] * rq * rq * pq[r]);
+        dKa[ct][r] = rk2 * (dKa[ct][r] - xk[ct][r] * rk2 * rk2 * pk[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < KT; ++ct) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dQa[ct][r]), rdq, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dKa[ct][r]), rdk, off, 0, 0);
+    }
+  }
+}
+
+}  // namespace gdn
+
+// ------------------------------------------------------------- host ----
+namespace gdn {
+
+template <int K, int V>
+static void launch_bwd_kernels(const uint16_t* q, const uint16_t* k, const uint16_t* qn,
+                               const uint16_t* kn, const uint16_t* v, const uint16_t* dO,
+                               const float* beta, const float* dht, float* dh0,
+                               const int32_t* cu, int B, int T, int Hqk, int Hv, int N,
+                               float scale, bool l2, const WsPlan& p, unsigned char* wsb,
+                               uint16_t* dq, uint16_t* dk, uint16_t* dv, float* dg,
+                               float* dbeta, hipStream_t st) {
+  BwdWs ws;
+  ws.f = ws_pointers(p, wsb);
+  ws.dse = reinterpret_cast<uint16_t*>(wsb + p.dse);
+  ws.dd = reinterpret_cast<uint16_t*>(wsb + p.dd);
+  const int total = B * T;
+  hipLaunchKernelGGL((chunk_rev_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, qn, kn,
+                     dO, dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  if (p.ncmax > 0)
+    hipLaunchKernelGGL((chunk_grad_kernel<K, V>), dim3((unsigned)p.ncmax, Hqk), dim3(256), 0,
+                       st, qn, kn, q, k, v, dO, beta, cu, N, T, total, Hqk, Hv, scale,
+                       l2 ? 1 : 0, ws, dq, dk, dv, dg, dbeta);
+}
+
+}  // namespace gdn
+
+namespace gdn_host {
+int validate_common(const void* q, const void* k, const void* v, const float* g,
+                    const float* beta, const float* h0, const float* ht, const void* o,
+                    const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N);
+}
+
+extern "C" size_t gdn_chunk_bwd_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
+                                                int N, int has_cu_seqlens, int use_qk_l2norm) {
+  if (B < 0 || T < 0 || Hqk <= 0 || Hv <= 0 || N < 0 || K <= 0 || V <= 0) return 0;
+  return gdn::plan_ws(B, T, Hqk, Hv, K, V, N, has_cu_seqlens != 0, use_qk_l2norm != 0, true)
+      .total;
+}
+
+extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g,
+                             const float* beta, const float* h0, const void* dO,
+                             const float* dht, void* dq, void* dk, void* dv, float* dg,
+                             float* dbeta, float* dh0, const int32_t* cu_seqlens, int B, int T,
+                             int Hqk, int Hv, int K, int V, int N, float scale,
+                             int use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  int rc = gdn_host::validate_common(q, k, v, g, beta, h0, nullptr, dO, cu_seqlens, B, T, Hqk,
+                                     Hv, K, V, N);
+  if (rc) return rc;
+  const long long tokens = (long long)B * T;
+  if (tokens > 0 && (!dq || !dk || !dv || !dg || !dbeta))
+    return gdn_host::fail(GDN_ERR_NULL, "gdn_chunk_bwd: dq, dk, dv, dg and dbeta must be non-NULL");
+  if (N == 0 || (tokens == 0 && !dh0)) return GDN_OK;
+  const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
+                                     use_qk_l2norm != 0, true);
+  if (!workspace || workspace_bytes < p.total)
+    return gdn_host::fail(GDN_ERR_WORKSPACE, "gdn_chunk_bwd: workspace needs " +
+                                                 std::to_string(p.total) + " bytes, got " +
+                                                 std::to_string(workspace_bytes));
+  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_bwd: problem too large");
+  auto* wsb = static_cast<unsigned char*>(workspace);
+  auto st = static_cast<hipStream_t>(stream);
+  auto* qq = static_cast<const uint16_t*>(q);
+  auto* kk = static_cast<const uint16_t*>(k);
+  auto* vv = static_cast<const uint16_t*>(v);
+  const bool l2 = use_qk_l2norm != 0;
+  // forward recomputation: prep (with T, Tb^T, P^T) and the chain saving the
+  // chunk-start states and the deltas
+  gdn::launch_chunk_fwd(qq, kk, vv, g, beta, h0, nullptr, nullptr, cu_seqlens, B, T, Hqk, Hv,
+                        K, V, N, scale, l2, true, p, wsb, st);
+  const uint16_t* qn = l2 ? reinterpret_cast<const uint16_t*>(wsb + p.qn) : qq;
+  const uint16_t* kn = l2 ? reinterpret_cast<const uint16_t*>(wsb + p.kn) : kk;
+  auto* ddo = static_cast<const uint16_t*>(dO);
+  auto* dqq = static_cast<uint16_t*>(dq);
+  auto* dkk = static_cast<uint16_t*>(dk);
+  auto* dvv = static_cast<uint16_t*>(dv);
+#define GDN_BWD(KK_, VV_)                                                                    \
+  gdn::launch_bwd_kernels<KK_, VV_>(qq, kk, qn, kn, vv, ddo, beta, dht, dh0, cu_seqlens, B, T, \
+                                    Hqk, Hv, N, scale, l2, p, wsb, dqq, dkk, dvv, dg, dbeta, st)
+  if (K == 128 && V == 128) GDN_BWD(128, 128);
+  else if (K == 128) GDN_BWD(128, 64);
+  else if (V == 128) GDN_BWD(64, 128);
+  else GDN_BWD(64, 64);
+#undef GDN_BWD
+  return gdn_host::check_launch("gdn_chunk_bwd");
+}

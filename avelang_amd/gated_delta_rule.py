@@ -26,8 +26,10 @@ from . import _native
 
 __all__ = [
     "chunk_gated_delta_rule",
+    "chunk_gated_delta_rule_bwd",
     "fused_recurrent_gated_delta_rule",
     "chunk_workspace_bytes",
+    "chunk_bwd_workspace_bytes",
 ]
 
 CHUNK_SIZE = 64
@@ -115,6 +117,105 @@ def chunk_workspace_bytes(B: int, T: int, Hqk: int, Hv: int, K: int, V: int, N: 
         B, T, Hqk, Hv, K, V, N, int(has_cu_seqlens), int(use_qk_l2norm)))
 
 
+def chunk_bwd_workspace_bytes(B: int, T: int, Hqk: int, Hv: int, K: int, V: int, N: int,
+                              has_cu_seqlens: bool, use_qk_l2norm: bool = False) -> int:
+    """Device scratch bytes ``chunk_gated_delta_rule_bwd`` needs (gdn_chunk_bwd_workspace_bytes)."""
+    return int(_native.lib().gdn_chunk_bwd_workspace_bytes(
+        B, T, Hqk, Hv, K, V, N, int(has_cu_seqlens), int(use_qk_l2norm)))
+
+
+def chunk_gated_delta_rule_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    do: torch.Tensor,
+    dht: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    *,
+    workspace: Optional[torch.Tensor] = None,
+):
+    """Gradients of ``chunk_gated_delta_rule`` (gdn_chunk_bwd).
+
+    ``do`` is dL/do (bf16, the shape of v); ``dht`` (nullable) is dL/d(final
+    state).  Returns ``(dq, dk, dv, dg, dbeta, dh0)``: dq, dk, dv in bf16,
+    dg, dbeta in fp32, dh0 fp32 (``None`` without ``initial_state``).  The
+    forward is recomputed from the inputs; nothing is kept from the forward
+    call.  With ``use_qk_l2norm_in_kernel`` dq and dk are gradients with
+    respect to the raw q and k.
+    """
+    name = "chunk_gated_delta_rule_bwd"
+    q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
+        q, k, v, g, beta, initial_state, cu_seqlens, name)
+    if scale is None:
+        scale = K ** -0.5
+    dev = q.device
+    if (not isinstance(do, torch.Tensor) or do.shape != v.shape or do.dtype != torch.bfloat16
+            or do.device != dev):
+        raise ValueError(f"{name}: do must be a bf16 tensor of shape {tuple(v.shape)} on {dev}.")
+    do = do.contiguous()
+    if dht is not None:
+        if (tuple(dht.shape) != (N, Hv, K, V) or dht.dtype != torch.float32
+                or dht.device != dev):
+            raise ValueError(f"{name}: dht must be fp32 {(N, Hv, K, V)} on {dev}.")
+        dht = dht.contiguous()
+    h0 = initial_state.contiguous() if initial_state is not None else None
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dg = torch.empty((B, T, Hv), dtype=torch.float32, device=dev)
+    dbeta = torch.empty((B, T, Hv), dtype=torch.float32, device=dev)
+    dh0 = torch.empty((N, Hv, K, V), dtype=torch.float32, device=dev) if h0 is not None else None
+    nbytes = chunk_bwd_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu is not None,
+                                       use_qk_l2norm_in_kernel)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < nbytes or workspace.device != dev:
+        raise ValueError(f"{name}: workspace must be >= {nbytes} bytes on {dev}.")
+    rc = _native.lib().gdn_chunk_bwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), _ptr(h0),
+        do.data_ptr(), _ptr(dht),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), dbeta.data_ptr(), _ptr(dh0),
+        _ptr(cu), B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream_ptr(dev))
+    _native.check(rc, name)
+    return dq, dk, dv, dg, dbeta, dh0
+
+
+class _ChunkGatedDeltaRule(torch.autograd.Function):
+    """Autograd form of chunk_gated_delta_rule: forward gdn_chunk_fwd,
+    backward gdn_chunk_bwd (the forward is recomputed, only inputs saved)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
+                use_qk_l2norm_in_kernel):
+        o, ht = _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state,
+                           cu_seqlens, use_qk_l2norm_in_kernel)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state, cu_seqlens)
+        ctx.scale = scale
+        ctx.l2 = use_qk_l2norm_in_kernel
+        ctx.g_dtype, ctx.beta_dtype = g.dtype, beta.dtype
+        ctx.has_ht = output_final_state
+        if output_final_state:
+            return o, ht
+        return o
+
+    @staticmethod
+    def backward(ctx, do, dht=None):
+        q, k, v, g, beta, h0, cu = ctx.saved_tensors
+        if dht is not None and not ctx.has_ht:
+            dht = None
+        dq, dk, dv, dg, db, dh0 = chunk_gated_delta_rule_bwd(
+            q, k, v, g, beta, do.to(torch.bfloat16), dht.float() if dht is not None else None,
+            ctx.scale, h0, cu, ctx.l2)
+        return (dq, dk, dv, dg.to(ctx.g_dtype), db.to(ctx.beta_dtype), None, dh0, None, None,
+                None)
+
+
 def chunk_gated_delta_rule(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -140,7 +241,29 @@ def chunk_gated_delta_rule(
     to avoid allocation; ``final_state`` may be ``initial_state`` itself.
     With ``use_qk_l2norm_in_kernel`` q and k are L2-normalised (eps 1e-6)
     and rounded to bf16 before use, as FLA's separate l2norm pass does.
+
+    Differentiable: when any of q, k, v, g, beta, initial_state requires
+    grad (and grad mode is on) the call goes through an autograd function
+    whose backward is ``chunk_gated_delta_rule_bwd`` (gdn_chunk_bwd).
     """
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (q, k, v, g, beta, initial_state)):
+        if out is not None or workspace is not None or final_state is not None:
+            raise ValueError("chunk_gated_delta_rule: out / workspace / final_state buffers "
+                             "are not supported when gradients are required.")
+        if scale is None:
+            scale = q.shape[-1] ** -0.5
+        res = _ChunkGatedDeltaRule.apply(q, k, v, g, beta, float(scale), initial_state,
+                                         bool(output_final_state), cu_seqlens,
+                                         bool(use_qk_l2norm_in_kernel))
+        return (res[0], res[1]) if output_final_state else (res, None)
+    return _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
+                      use_qk_l2norm_in_kernel, workspace=workspace, out=out,
+                      final_state=final_state)
+
+
+def _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
+               use_qk_l2norm_in_kernel, workspace=None, out=None, final_state=None):
     name = "chunk_gated_delta_rule"
     q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
         q, k, v, g, beta, initial_state, cu_seqlens, name)

@@ -9,7 +9,7 @@
  * driver.py:220-392, stream getter backends/driver.py:24-30).  These entry
  * points take the place of that launcher for the two GDN operators that
  * Qwen3-Next calls (transformers modeling_qwen3_next.py:658-683):
- *   chunk_gated_delta_rule            -> gdn_chunk_fwd
+ *   chunk_gated_delta_rule            -> gdn_chunk_fwd (backward: gdn_chunk_bwd)
  *   fused_recurrent_gated_delta_rule  -> gdn_recurrent_fwd
  *
  * Conventions (all entry points):
@@ -92,6 +92,43 @@ int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
                       int B, int T, int Hqk, int Hv, int K, int V, int N,
                       float scale, int use_qk_l2norm,
                       void* stream);
+
+/*
+ * Chunked backward (chunk = 64 tokens): gradients of gdn_chunk_fwd's o and
+ * final state with respect to q, k, v, g, beta and h0.  Replaces the
+ * backward launch of FLA's autograd chunk_gated_delta_rule (the operator
+ * Qwen3-Next trains through, modeling_qwen3_next.py:672-683); the
+ * reference repository has no counterpart (its kernel library,
+ * python/avelang_kernels/, is forward-only and holds one GEMM).
+ *
+ * Recomputes the forward from (q, k, v, g, beta, h0) -- nothing has to be
+ * kept from the forward call -- then runs the state gradient backwards over
+ * the chunks and forms every chunk's local gradients in parallel.
+ *
+ *   dO    [B, T, Hv, V] bf16: dL/do.
+ *   dht   nullable: dL/d(final state) [N, Hv, K, V] fp32; NULL = zeros.
+ *   dq, dk [B, T, Hqk, K] bf16 (summed over each qk-head's v-heads);
+ *   dv    [B, T, Hv, V] bf16;  dg, dbeta [B, T, Hv] fp32.
+ *   dh0   nullable: dL/dh0 [N, Hv, K, V] fp32 (written even when h0 is NULL:
+ *         the gradient with respect to a zero initial state).
+ *   use_qk_l2norm != 0: the forward normalised q and k; dq and dk are the
+ *         gradients with respect to the raw (unnormalised) q and k.
+ *   workspace: at least gdn_chunk_bwd_workspace_bytes(...).
+ * Every output is fully overwritten (no accumulation into it).
+ */
+int gdn_chunk_bwd(const void* q, const void* k, const void* v,
+                  const float* g, const float* beta, const float* h0,
+                  const void* dO, const float* dht,
+                  void* dq, void* dk, void* dv, float* dg, float* dbeta, float* dh0,
+                  const int32_t* cu_seqlens,
+                  int B, int T, int Hqk, int Hv, int K, int V, int N,
+                  float scale, int use_qk_l2norm,
+                  void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Bytes of device workspace gdn_chunk_bwd needs for these sizes. */
+size_t gdn_chunk_bwd_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
+                                     int N, int has_cu_seqlens, int use_qk_l2norm);
 
 /* Thread-local message describing the last failure (never NULL). */
 const char* gdn_last_error(void);

@@ -26,7 +26,8 @@ def _declared(headers=("gdn.h", "gdn_layer.h")):
 
 
 def test_header_declares_expected_entry_points():
-    assert _declared(("gdn.h",)) == ["gdn_abi_version", "gdn_chunk_fwd",
+    assert _declared(("gdn.h",)) == ["gdn_abi_version", "gdn_chunk_bwd",
+                                     "gdn_chunk_bwd_workspace_bytes", "gdn_chunk_fwd",
                                      "gdn_chunk_workspace_bytes", "gdn_last_error",
                                      "gdn_recurrent_fwd"]
     assert _declared(("gdn_layer.h",)) == [
@@ -39,7 +40,7 @@ def test_every_declared_symbol_is_exported(lib):
     for name in _declared():
         assert hasattr(lib, name), name
     assert set(_native.EXPORTS) == set(_declared())
-    assert lib.gdn_abi_version() == 100
+    assert lib.gdn_abi_version() == 101
 
 
 def _rec(lib, **kw):
