@@ -338,13 +338,14 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
 namespace gdn {
 
 // --------------------------------------------------- gradient kernel ----
-// One workgroup per (chunk, qk-head); wave w owns chunk rows 16w..16w+15 of
-// every [64 x *] result.  "OL" = the MFMA output layout: lane (r16, grp)
-// holds rows 16w + 4grp + r (r = 0..3) of column 16ct + r16.
+// One workgroup of 8 waves per (chunk, qk-head).  Wave w8 owns row tile
+// rt = w8 % 4 (chunk rows 16rt..16rt+15) and the column tiles of parity
+// hf = w8 / 4 of every [64 x *] result.  "OL" = the MFMA output layout:
+// lane (r16, grp) holds rows 16rt + 4grp + r (r = 0..3) of column 16ct + r16.
 //
 // Local gradients of one (chunk, v-head) given S (chunk start state), dS'
 // (gradient into its end state), d and dd (all bf16 from the chains):
-//   R1 = dO S^T, R2 = dd S^T, dKt = d dS'^T              (streamed, no LDS)
+//   R1 = dO S^T, R2 = dd S^T, dKt = d dS'^T
 //   dPt = lower_incl(c' dO d^T),  dT = dd (bV)^T - R2 (b e^G K)^T
 //   dA = strict_lower(-T^T dT T^T)                       (fp32 MFMA)
 //   M = dA * b_i Gam,  MP = dPt * Gam
@@ -356,9 +357,17 @@ namespace gdn {
 //        (+ e^G_L <S, dS'> + sum(rho) on the last row),
 //   X = (b_i dA KK + dPt QK) Gam,  rho_j = e^(G_L - G_j) K_j . dKt_j
 //   dg = reverse cumsum of dG within the chunk.
-// (c' is folded into dO: dPt and R1 use c' dO.)
+// (c' is folded into dO: dPt and R1 use c' dO.)  V . (T^T dd) is formed as
+// the column sums of T * (dd V^T), since (T^T dd)_i . V_i = sum_j T_ji (dd V^T)_ji.
+//
+// Every operand read by rows (S, dS' by state rows; d, V by token rows)
+// streams through a double-buffered LDS stage of 32 rows: slice s + 1 is
+// written to the free stage before slice s is multiplied, while slice
+// s + 3 is already requested into registers.
+constexpr int kGradThreads = 512;
+
 template <int K, int V>
-__global__ __launch_bounds__(256) void chunk_grad_kernel(
+__global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ qraw, const uint16_t* __restrict__ kraw,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dO,
@@ -366,10 +375,17 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
     int Hqk, int Hv, float scale, int l2norm, BwdWs ws, uint16_t* __restrict__ dq,
     uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, float* __restrict__ dg,
     float* __restrict__ dbeta) {
+  constexpr int NTH = kGradThreads;
   constexpr int KT = K / 16, VT = V / 16, KB = K / 32, VB = V / 32;
+  constexpr int KH = KT / 2, VH = VT / 2;   // column tiles per wave
   constexpr int LK = K + 8, LV = V + 8, LT = 68, LC = 72;
+  constexpr int NSS = K / 32;          // slices of S / dS' (32 state rows each)
+  constexpr int NSL = NSS + 2;         // + two slices of d / V (32 token rows each)
+  constexpr int NPOS = 32 * V / 8;     // 16-byte positions of one matrix in a slice
+  static_assert(NPOS <= NTH, "one staged position per thread");
   __shared__ __attribute__((aligned(16))) uint16_t Ks[64][LK];
   __shared__ __attribute__((aligned(16))) uint16_t Qs[64][LK];
+  __shared__ __attribute__((aligned(16))) uint16_t Stg[2][2][32][LV];   // [buf][matrix][row]
   __shared__ __attribute__((aligned(16))) float T32[64][LT];
   __shared__ __attribute__((aligned(16))) float X32[64][LT];
   __shared__ __attribute__((aligned(16))) uint16_t Tb16[64][LC];
@@ -385,8 +401,10 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
   __shared__ __attribute__((aligned(16))) float Cs[64];     // column sums of X
+  __shared__ __attribute__((aligned(16))) float Cv[64];     // column sums of T * (dd V^T)
   __shared__ __attribute__((aligned(16))) float Ds[64];     // dG per row
-  __shared__ float Red[4];
+  __shared__ __attribute__((aligned(16))) float RowP[2][5][64];   // row partials per half
+  __shared__ float Red[8];
 
   const int ci = blockIdx.x;
   const int hq = blockIdx.y;
@@ -412,10 +430,12 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
   const int L = min(kChunk, e - t0);
   const int Gn = Hv / Hqk;
 
-  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const int tid = threadIdx.x, lane = tid % 64;
+  const int w8 = __builtin_amdgcn_readfirstlane(tid / 64);   // wave index (scalar)
+  const int rt = w8 & 3, hf = w8 >> 2;
   const int r16 = lane % 16, grp = lane / 16;
-  const int rowA = 16 * w + r16;          // A-fragment row of this lane
-  const int row0 = 16 * w + 4 * grp;      // first OL row of this lane
+  const int rowA = 16 * rt + r16;         // A-fragment row of this lane
+  const int row0 = 16 * rt + 4 * grp;     // first OL row of this lane
 
   // K / Q rows of the chunk (rows >= L read as zero)
   const int qkbytes = L * Hqk * K * 2;
@@ -423,63 +443,60 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
       const_cast<uint16_t*>(k + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(q + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
-  for (int idx = tid; idx < 64 * K / 8; idx += 256) {
-    const int r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
-    const int off = (r * Hqk * K + c8) * 2;
-    *reinterpret_cast<u16x8*>(&Ks[r][c8]) =
-        __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-    *reinterpret_cast<u16x8*>(&Qs[r][c8]) =
-        __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+  {
+    constexpr int NQ = 64 * K / 8 / NTH;   // 16-byte chunks per thread
+    u16x8 kr[NQ], qr[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int idx = tid + NTH * i, r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
+      const int off = (r * Hqk * K + c8) * 2;
+      kr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+      qr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int idx = tid + NTH * i, r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
+      *reinterpret_cast<u16x8*>(&Ks[r][c8]) = kr[i];
+      *reinterpret_cast<u16x8*>(&Qs[r][c8]) = qr[i];
+    }
   }
   __syncthreads();
 
-  // K K^T and Q K^T in OL (shared by the group's v-heads)
-  f32x4 kk[4], qk[4];
-  {
-    u16x8 ka[KB], qa[KB];
+  f32x4 dQa[KH], dKa[KH];   // column tiles 2m + hf
 #pragma unroll
-    for (int b = 0; b < KB; ++b) {
-      ka[b] = *reinterpret_cast<const u16x8*>(&Ks[rowA][32 * b + 8 * grp]);
-      qa[b] = *reinterpret_cast<const u16x8*>(&Qs[rowA][32 * b + 8 * grp]);
-    }
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      kk[ct] = zero4();
-      qk[ct] = zero4();
-#pragma unroll
-      for (int b = 0; b < KB; ++b) {
-        const u16x8 kb = *reinterpret_cast<const u16x8*>(&Ks[16 * ct + r16][32 * b + 8 * grp]);
-        kk[ct] = mfma16(ka[b], kb, kk[ct]);
-        qk[ct] = mfma16(qa[b], kb, qk[ct]);
-      }
-    }
-  }
-
-  f32x4 dQa[KT], dKa[KT];
-#pragma unroll
-  for (int ct = 0; ct < KT; ++ct) {
-    dQa[ct] = zero4();
-    dKa[ct] = zero4();
+  for (int m = 0; m < KH; ++m) {
+    dQa[m] = zero4();
+    dKa[m] = zero4();
   }
 
   const int vbytes = L * Hv * V * 2;
   for (int gi = 0; gi < Gn; ++gi) {
+    // The lane index is passed through an empty asm statement once per
+    // v-head, so the many per-lane LDS / buffer addresses derived from it are
+    // formed inside the loop where they are used, instead of being hoisted
+    // out of it (live across the whole loop they exceed the register file and
+    // spill; the spill reloads then wait on every outstanding store).
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid % 64;
+    const int w8 = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int rt = w8 & 3, hf = w8 >> 2;
+    const int r16 = lane % 16, grp = lane / 16;
+    const int rowA = 16 * rt + r16;
+    const int row0 = 16 * rt + 4 * grp;
+    // staged position of this thread in a slice (both matrices)
+    const bool stager = tid < NPOS;
+    const int sp_r = (tid % NPOS) / (V / 8), sp_c8 = 8 * (tid % (V / 8));
+    const int sp_vs = (sp_r * V + sp_c8) * 2;            // byte offset in a state slice
+    const int sp_vt = (sp_r * Hv * V + sp_c8) * 2;       // byte offset in a token slice
     const int h = hq * Gn + gi;
     const size_t ch = (size_t)ci * Hv + h;
-    // ---- per-v-head operands into LDS: T (fp32 + bf16), G, beta, dd rows
-    {
-      const float* tsrc = ws.f.tmat + ch * 64 * 64;
-      for (int idx = tid; idx < 64 * 16; idx += 256) {
-        const int r = idx / 16, c4 = 4 * (idx % 16);
-        const f32x4 x = *reinterpret_cast<const f32x4*>(tsrc + r * 64 + c4);
-        *reinterpret_cast<f32x4*>(&T32[r][c4]) = x;
-        *reinterpret_cast<u16x4*>(&Tb16[r][c4]) = f2bf4(x);
-      }
-      if (tid < 64) {
-        Gs[tid] = ws.f.gate[ch * 64 + tid];
-        Bs[tid] = tid < L ? beta[(size_t)(t0 + tid) * Hv + h] : 0.f;
-      }
-    }
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
+        ws.f.hs + ch * K * V, 0, K * V * 2, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rE = __builtin_amdgcn_make_buffer_rsrc(
+        ws.dse + ch * K * V, 0, K * V * 2, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rT = __builtin_amdgcn_make_buffer_rsrc(
+        ws.f.tmat + ch * 64 * 64, 0, 64 * 64 * 4, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdd = __builtin_amdgcn_make_buffer_rsrc(
         ws.dd + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
@@ -488,12 +505,57 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
         const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
-    for (int idx = tid; idx < 64 * V / 8; idx += 256) {
-      const int r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
-      *reinterpret_cast<u16x8*>(&dds[r][c8]) = __builtin_bit_cast(
-          u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, (r * Hv * V + c8) * 2, 0, 0));
+
+    // slice sl: rows 32 sl.. of S (matrix 0) and dS' (matrix 1) for sl < NSS,
+    // token rows 32 (sl - NSS).. of d (0) and V (1) after
+    float sde = 0.f;   // partial <S, dS'> of the positions this thread stages
+    auto load_slice = [&](int sl, u16x8 (&buf)[2]) {
+      if (!stager) return;
+      if (sl < NSS) {
+        const int so = 32 * sl * V * 2;
+        buf[0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rS, sp_vs, so, 0));
+        buf[1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rE, sp_vs, so, 0));
+      } else {
+        const int so = 32 * (sl - NSS) * Hv * V * 2;
+        buf[0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_vt, so, 0));
+        buf[1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, sp_vt, so, 0));
+      }
+    };
+    auto store_slice = [&](int sl, const u16x8 (&buf)[2]) {
+      if (!stager) return;
+      *reinterpret_cast<u16x8*>(&Stg[sl & 1][0][sp_r][sp_c8]) = buf[0];
+      *reinterpret_cast<u16x8*>(&Stg[sl & 1][1][sp_r][sp_c8]) = buf[1];
+      if (sl < NSS) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sde += bf2f(buf[0][j]) * bf2f(buf[1][j]);
+      }
+    };
+
+    // ---- issued before the first wait: slices 0..2, T, G, beta, dd rows,
+    // the A fragments
+    u16x8 pre[3][2];
+    load_slice(0, pre[0]);
+    load_slice(1, pre[1]);
+    if (NSL > 2) load_slice(2, pre[2]);
+    constexpr int NT = 64 * 16 / NTH, ND = 64 * V / 8 / NTH;
+    f32x4 tv[NT];
+    u16x8 dv8[ND];
+    {
+#pragma unroll
+      for (int i = 0; i < NT; ++i)
+        tv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rT, 16 * tid, 16 * NTH * i, 0));
+#pragma unroll
+      for (int i = 0; i < ND; ++i) {
+        const int idx = tid + NTH * i, r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
+        dv8[i] = __builtin_bit_cast(
+            u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, (r * Hv * V + c8) * 2, 0, 0));
+      }
     }
-    // A fragments (rows rowA): dO, dd, d
+    float gsv = 0.f, bsv = 0.f;
+    if (tid < 64) {
+      gsv = ws.f.gate[ch * 64 + tid];
+      bsv = tid < L ? beta[(size_t)(t0 + min(tid, L - 1)) * Hv + h] : 0.f;
+    }
     u16x8 aO[VB], aD[VB], aL[VB];
 #pragma unroll
     for (int b = 0; b < VB; ++b) {
@@ -501,6 +563,23 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
       aO[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
       aD[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, off, 0, 0));
       aL[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    store_slice(0, pre[0]);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const int idx = tid + NTH * i, r = idx / 16, c4 = 4 * (idx % 16);
+      *reinterpret_cast<f32x4*>(&T32[r][c4]) = tv[i];
+      *reinterpret_cast<u16x4*>(&Tb16[r][c4]) = f2bf4(tv[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int idx = tid + NTH * i, r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
+      *reinterpret_cast<u16x8*>(&dds[r][c8]) = dv8[i];
+    }
+    if (tid < 64) {
+      Gs[tid] = gsv;
+      Bs[tid] = bsv;
     }
     __syncthreads();
 
@@ -513,63 +592,60 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
       dec[r] = __expf(GL - Gs[row0 + r]);
       bt[r] = Bs[row0 + r];
     }
-    f32x4 qr1 = zero4(), rho = zero4(), ktw = zero4(), vtu = zero4();
+    f32x4 qr1 = zero4(), rho = zero4(), ktw = zero4();
 
-    // ---- streamed products against S and dS' (rows of [K][V], bf16)
-    const uint16_t* Sg = ws.f.hs + ch * K * V;
-    const uint16_t* Eg = ws.dse + ch * K * V;
-    float sde = 0.f;   // partial <S, dS'>
+    // ---- streamed products over the slices (this wave: column tile hf of
+    // each slice)
+    f32x4 dpt[2], ddv[2];
 #pragma unroll
-    for (int ct = 0; ct < KT; ++ct) {
-      f32x4 r1 = zero4(), r2 = zero4(), dkt = zero4();
+    for (int sl = 0; sl < NSL; ++sl) {
+      if (sl + 1 < NSL) store_slice(sl + 1, pre[(sl + 1) % 3]);
+      if (sl + 3 < NSL) load_slice(sl + 3, pre[(sl + 3) % 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      const int bufi = sl & 1;
+      f32x4 x0 = zero4(), x1 = zero4(), x2 = zero4();
 #pragma unroll
       for (int b = 0; b < VB; ++b) {
-        const size_t boff = (size_t)(16 * ct + r16) * V + 32 * b + 8 * grp;
-        const u16x8 sb = *reinterpret_cast<const u16x8*>(Sg + boff);
-        const u16x8 eb = *reinterpret_cast<const u16x8*>(Eg + boff);
-        r1 = mfma16(aO[b], sb, r1);
-        r2 = mfma16(aD[b], sb, r2);
-        dkt = mfma16(aL[b], eb, dkt);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sde += bf2f(sb[i]) * bf2f(eb[i]);
+        const u16x8 b0 = *reinterpret_cast<const u16x8*>(&Stg[bufi][0][16 * hf + r16][32 * b + 8 * grp]);
+        const u16x8 b1 = *reinterpret_cast<const u16x8*>(&Stg[bufi][1][16 * hf + r16][32 * b + 8 * grp]);
+        if (sl < NSS) {
+          x0 = mfma16(aO[b], b0, x0);    // dO S^T
+          x1 = mfma16(aD[b], b0, x1);    // dd S^T
+          x2 = mfma16(aL[b], b1, x2);    // d dS'^T
+        } else {
+          x0 = mfma16(aO[b], b0, x0);    // dO d^T
+          x1 = mfma16(aD[b], b1, x1);    // dd V^T
+        }
       }
+      if (sl < NSS) {
+        const int ct = 2 * sl + hf;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float qv = bf2f(Qs[row0 + r][16 * ct + r16]);
-        const float kv = bf2f(Ks[row0 + r][16 * ct + r16]);
-        const float a = scale * r1[r];
-        dQa[ct][r] += eg[r] * a;
-        qr1[r] += qv * a;
-        const float d2 = dec[r] * dkt[r];
-        dKa[ct][r] += d2;
-        rho[r] += kv * d2;
-        R2s[row0 + r][16 * ct + r16] = f2bf(r2[r]);
+        for (int r = 0; r < 4; ++r) {
+          const float qv = bf2f(Qs[row0 + r][16 * ct + r16]);
+          const float kv = bf2f(Ks[row0 + r][16 * ct + r16]);
+          const float a = scale * x0[r];
+          dQa[sl][r] += eg[r] * a;
+          qr1[r] += qv * a;
+          const float d2 = dec[r] * x2[r];
+          dKa[sl][r] += d2;
+          rho[r] += kv * d2;
+          R2s[row0 + r][16 * ct + r16] = f2bf(x1[r]);
+        }
+      } else {
+        dpt[sl - NSS] = x0;
+        ddv[sl - NSS] = x1;
       }
+      __syncthreads();
     }
-    // dPt = c' dO d^T and dd V^T (C x C, OL)
-    f32x4 dpt[4], ddv[4];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      dpt[ct] = zero4();
-      ddv[ct] = zero4();
-#pragma unroll
-      for (int b = 0; b < VB; ++b) {
-        const int off = ((16 * ct + r16) * Hv * V + 32 * b + 8 * grp) * 2;
-        const u16x8 lb = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
-        const u16x8 vb = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
-        dpt[ct] = mfma16(aO[b], lb, dpt[ct]);
-        ddv[ct] = mfma16(aD[b], vb, ddv[ct]);
-      }
-    }
-    __syncthreads();   // R2s complete
 
-    // ---- dT = dd (bV)^T - R2 (b e^G K)^T  -> X32 (fp32)
+    // ---- dT = dd (bV)^T - R2 (b e^G K)^T  -> X32 (fp32), tiles 2m + hf
     {
       u16x8 a2[KB];
 #pragma unroll
       for (int b = 0; b < KB; ++b) a2[b] = *reinterpret_cast<const u16x8*>(&R2s[rowA][32 * b + 8 * grp]);
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
+      for (int m = 0; m < 2; ++m) {
+        const int ct = 2 * m + hf;
         f32x4 t2 = zero4();
 #pragma unroll
         for (int b = 0; b < KB; ++b)
@@ -577,32 +653,31 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
         const int j = 16 * ct + r16;
         const float bj = Bs[j], bgj = bj * __expf(Gs[j]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) X32[row0 + r][j] = ddv[ct][r] * bj - t2[r] * bgj;
+        for (int r = 0; r < 4; ++r) X32[row0 + r][j] = ddv[m][r] * bj - t2[r] * bgj;
       }
     }
-    // ---- T^T dd (-> dv, dbeta) and T^T dW = -T^T R2 (-> dk, dbeta, dG)
+    // ---- T^T dd (-> dv) and T^T dW = -T^T R2 (-> dk, dbeta, dG)
     {
       u16x8 ta[2];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) ta[b] = lds_colfrag(&Tb16[0][0], LC, 32 * b, 16 * w, lane);
+      for (int b = 0; b < 2; ++b) ta[b] = lds_colfrag(&Tb16[0][0], LC, 32 * b, 16 * rt, lane);
       const __amdgpu_buffer_rsrc_t rdv = __builtin_amdgcn_make_buffer_rsrc(
           dv + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
 #pragma unroll
-      for (int ct = 0; ct < VT; ++ct) {
+      for (int m = 0; m < VH; ++m) {
+        const int ct = 2 * m + hf;
         f32x4 tu = zero4();
 #pragma unroll
         for (int b = 0; b < 2; ++b)
           tu = mfma16(ta[b], lds_colfrag(&dds[0][0], LV, 32 * b, 16 * ct, lane), tu);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float vv = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rv, ((row0 + r) * Hv * V + 16 * ct + r16) * 2, 0, 0));
-          vtu[r] += vv * tu[r];
+        for (int r = 0; r < 4; ++r)
           __builtin_amdgcn_raw_buffer_store_b16(f2bf(bt[r] * tu[r]), rdv,
                                                 ((row0 + r) * Hv * V + 16 * ct + r16) * 2, 0, 0);
-        }
       }
 #pragma unroll
-      for (int ct = 0; ct < KT; ++ct) {
+      for (int m = 0; m < KH; ++m) {
+        const int ct = 2 * m + hf;
         f32x4 tw = zero4();
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -610,7 +685,7 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float x = -tw[r];   // (T^T dW)
-          dKa[ct][r] += bt[r] * eg[r] * x;
+          dKa[m][r] += bt[r] * eg[r] * x;
           ktw[r] += bf2f(Ks[row0 + r][16 * ct + r16]) * x;
         }
       }
@@ -618,70 +693,100 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
     __syncthreads();   // X32 = dT complete; dd / R2 no longer needed
 
     // ---- dA = strict_lower(-T^T (dT T^T)) on fp32 MFMA (T lower triangular)
-    f32x4 m1[4];
+    f32x4 m1[2];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      m1[ct] = zero4();
+    for (int m = 0; m < 2; ++m) {
+      const int ct = 2 * m + hf;
+      m1[m] = zero4();
       for (int j0 = 0; j0 < 16 * (ct + 1); j0 += 4)
-        m1[ct] = mfma4f32(X32[rowA][j0 + grp], T32[16 * ct + r16][j0 + grp], m1[ct]);
+        m1[m] = mfma4f32(X32[rowA][j0 + grp], T32[16 * ct + r16][j0 + grp], m1[m]);
     }
     __syncthreads();
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) X32[row0 + r][16 * ct + r16] = m1[ct][r];
+      for (int r = 0; r < 4; ++r) X32[row0 + r][16 * (2 * m + hf) + r16] = m1[m][r];
     __syncthreads();
-    f32x4 da[4];
+    f32x4 da[2];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      da[ct] = zero4();
-      if (ct <= w) {
-        for (int j0 = 16 * w; j0 < 64; j0 += 4)
-          da[ct] = mfma4f32(T32[j0 + grp][rowA], X32[j0 + grp][16 * ct + r16], da[ct]);
+    for (int m = 0; m < 2; ++m) {
+      const int ct = 2 * m + hf;
+      da[m] = zero4();
+      if (ct <= rt) {
+        for (int j0 = 16 * rt; j0 < 64; j0 += 4)
+          da[m] = mfma4f32(T32[j0 + grp][rowA], X32[j0 + grp][16 * ct + r16], da[m]);
       }
     }
     __syncthreads();   // X32 (M1) reads done before X is written there
 
-    // ---- C x C elementwise: M, MP, dbeta / dG terms, X
+    // ---- K K^T and Q K^T (OL, this wave's two column tiles)
+    f32x4 kk[2], qk[2];
+    {
+      u16x8 ka[KB], qa[KB];
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        ka[b] = *reinterpret_cast<const u16x8*>(&Ks[rowA][32 * b + 8 * grp]);
+        qa[b] = *reinterpret_cast<const u16x8*>(&Qs[rowA][32 * b + 8 * grp]);
+      }
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int ct = 2 * m + hf;
+        kk[m] = zero4();
+        qk[m] = zero4();
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+          const u16x8 kb = *reinterpret_cast<const u16x8*>(&Ks[16 * ct + r16][32 * b + 8 * grp]);
+          kk[m] = mfma16(ka[b], kb, kk[m]);
+          qk[m] = mfma16(qa[b], kb, qk[m]);
+        }
+      }
+    }
+    // ---- C x C elementwise: M, MP, dbeta / dG terms, X; T * (dd V^T) for Cv
     f32x4 dba = zero4(), xr = zero4();
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const int j = 16 * ct + r16;
+    for (int m = 0; m < 2; ++m) {
+      const int j = 16 * (2 * m + hf) + r16;
       const float Gj = Gs[j];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = row0 + r;
         const float gam = (j <= i) ? __expf(Gs[i] - Gj) : 0.f;
-        const float dA = (j < i) ? -da[ct][r] : 0.f;
-        const float dP = (j <= i) ? scale * dpt[ct][r] : 0.f;
+        const float dA = (j < i) ? -da[m][r] : 0.f;
+        const float dP = (j <= i) ? scale * dpt[m][r] : 0.f;
         Ms[i][j] = f2bf(dA * bt[r] * gam);
         MPs[i][j] = f2bf(dP * gam);
-        dba[r] += dA * kk[ct][r] * gam;
-        const float x = (dA * bt[r] * kk[ct][r] + dP * qk[ct][r]) * gam;
+        dba[r] += dA * kk[m][r] * gam;
+        const float x = (dA * bt[r] * kk[m][r] + dP * qk[m][r]) * gam;
         xr[r] += x;
         X32[i][j] = x;
+        T32[i][j] *= ddv[m][r];   // T_ij (dd V^T)_ij, summed over i for column j below
       }
     }
     __syncthreads();
     if (tid < 64) {
-      float c = 0.f;
-      for (int i = 0; i < 64; ++i) c += X32[i][tid];
+      float c = 0.f, cv = 0.f;
+      for (int i = 0; i < 64; ++i) {
+        c += X32[i][tid];
+        cv += T32[i][tid];
+      }
       Cs[tid] = c;
+      Cv[tid] = cv;
     }
 
-    // ---- dK += M K + M^T K + MP^T Q,  dQ += MP K
+    // ---- dK += M K + M^T K + MP^T Q,  dQ += MP K (this wave's column tiles)
     {
       u16x8 am[2], amt[2], ap[2], apt[2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         am[b] = *reinterpret_cast<const u16x8*>(&Ms[rowA][32 * b + 8 * grp]);
         ap[b] = *reinterpret_cast<const u16x8*>(&MPs[rowA][32 * b + 8 * grp]);
-        amt[b] = lds_colfrag(&Ms[0][0], LC, 32 * b, 16 * w, lane);
-        apt[b] = lds_colfrag(&MPs[0][0], LC, 32 * b, 16 * w, lane);
+        amt[b] = lds_colfrag(&Ms[0][0], LC, 32 * b, 16 * rt, lane);
+        apt[b] = lds_colfrag(&MPs[0][0], LC, 32 * b, 16 * rt, lane);
       }
 #pragma unroll
-      for (int ct = 0; ct < KT; ++ct) {
-        f32x4 a0 = dKa[ct], a1 = zero4(), a2 = dQa[ct];
+      for (int m = 0; m < KH; ++m) {
+        const int ct = 2 * m + hf;
+        f32x4 a0 = dKa[m], a1 = zero4(), a2 = dQa[m];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
           const u16x8 kc = lds_colfrag(&Ks[0][0], LK, 32 * b, 16 * ct, lane);
@@ -691,12 +796,13 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
           a1 = mfma16(apt[b], qc, a1);
           a2 = mfma16(ap[b], kc, a2);
         }
-        dKa[ct] = a0 + a1;
-        dQa[ct] = a2;
+        dKa[m] = a0 + a1;
+        dQa[m] = a2;
       }
     }
 
-    // ---- row reductions over the 16 lanes of a group, dG, dbeta
+    // ---- row partials: reduce over the 16 lanes of a group, then combine
+    // the two column halves through LDS
 #pragma unroll
     for (int sh = 1; sh < 16; sh *= 2) {
 #pragma unroll
@@ -704,42 +810,49 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
         qr1[r] += __shfl_xor(qr1[r], sh);
         rho[r] += __shfl_xor(rho[r], sh);
         ktw[r] += __shfl_xor(ktw[r], sh);
-        vtu[r] += __shfl_xor(vtu[r], sh);
         dba[r] += __shfl_xor(dba[r], sh);
         xr[r] += __shfl_xor(xr[r], sh);
       }
     }
-    // sum of rho over all rows and <S, dS'> (wave sums, then across waves)
-    float rs = (r16 == 0) ? (rho[0] + rho[1] + rho[2] + rho[3]) : 0.f;
-#pragma unroll
-    for (int sh = 16; sh < 64; sh *= 2) rs += __shfl_xor(rs, sh);
+    if (r16 == 0) {
+      *reinterpret_cast<f32x4*>(&RowP[hf][0][row0]) = qr1;
+      *reinterpret_cast<f32x4*>(&RowP[hf][1][row0]) = rho;
+      *reinterpret_cast<f32x4*>(&RowP[hf][2][row0]) = ktw;
+      *reinterpret_cast<f32x4*>(&RowP[hf][3][row0]) = dba;
+      *reinterpret_cast<f32x4*>(&RowP[hf][4][row0]) = xr;
+    }
 #pragma unroll
     for (int sh = 1; sh < 64; sh *= 2) sde += __shfl_xor(sde, sh);
-    if (lane == 0) Red[w] = rs;
-    __syncthreads();   // Cs, Red complete
-    const float rho_all = Red[0] + Red[1] + Red[2] + Red[3];
-    if (r16 == 0) {
+    if (lane == 0) Red[w8] = sde;
+    __syncthreads();   // Cs, Cv, RowP, Red complete
+    if (w8 == 0) {
+      // per row (lane = row): total dG and dbeta, then dg = reverse cumsum
+      const int i = lane;
+      float sd = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = row0 + r;
-        float dG = eg[r] * qr1[r] - rho[r] + bt[r] * eg[r] * ktw[r] + xr[r] - Cs[i];
-        if (i == L - 1) dG += __expf(GL) * sde + rho_all;
-        Ds[i] = i < L ? dG : 0.f;
-        if (i < L)
-          dbeta[(size_t)(t0 + i) * Hv + h] = vtu[r] + eg[r] * ktw[r] + dba[r];
-      }
-    }
-    __syncthreads();
-    if (w == 0) {
-      // dg_i = sum_{m >= i} dG_m (reverse inclusive scan over the chunk)
-      float x = Ds[63 - lane];
+      for (int x = 0; x < 8; ++x) sd += Red[x];
+      const float rq1 = RowP[0][0][i] + RowP[1][0][i];
+      const float rrho = RowP[0][1][i] + RowP[1][1][i];
+      const float rktw = RowP[0][2][i] + RowP[1][2][i];
+      const float rdba = RowP[0][3][i] + RowP[1][3][i];
+      const float rxr = RowP[0][4][i] + RowP[1][4][i];
+      float rho_all = rrho;
+#pragma unroll
+      for (int sh = 1; sh < 64; sh *= 2) rho_all += __shfl_xor(rho_all, sh);
+      const float egi = __expf(Gs[i]), bi = Bs[i];
+      float dG = egi * rq1 - rrho + bi * egi * rktw + rxr - Cs[i];
+      if (i == L - 1) dG += __expf(GL) * sd + rho_all;
+      if (i < L) dbeta[(size_t)(t0 + i) * Hv + h] = Cv[i] + egi * rktw + rdba;
+      float x = i < L ? dG : 0.f;
+      // reverse inclusive scan over the 64 rows
+      x = __shfl(x, 63 - lane);
 #pragma unroll
       for (int d = 1; d < 64; d *= 2) {
         const float o = __shfl_up(x, d);
         if (lane >= d) x += o;
       }
-      const int i = 63 - lane;
-      if (i < L) dg[(size_t)(t0 + i) * Hv + h] = x;
+      const int ir = 63 - lane;
+      if (ir < L) dg[(size_t)(t0 + ir) * Hv + h] = x;
     }
     __syncthreads();   // LDS reuse by the next v-head
   }
@@ -755,18 +868,19 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
     const __amdgpu_buffer_rsrc_t rkr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(kraw + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
     f32x4 sq = zero4(), sk = zero4(), pq = zero4(), pk = zero4();
-    float xq[KT][4], xk[KT][4];
+    float xq[KH][4], xk[KH][4];
 #pragma unroll
-    for (int ct = 0; ct < KT; ++ct) {
+    for (int m = 0; m < KH; ++m) {
+      const int ct = 2 * m + hf;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
-        xq[ct][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rqr, off, 0, 0));
-        xk[ct][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rkr, off, 0, 0));
-        sq[r] += xq[ct][r] * xq[ct][r];
-        sk[r] += xk[ct][r] * xk[ct][r];
-        pq[r] += xq[ct][r] * dQa[ct][r];
-        pk[r] += xk[ct][r] * dKa[ct][r];
+        xq[m][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rqr, off, 0, 0));
+        xk[m][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rkr, off, 0, 0));
+        sq[r] += xq[m][r] * xq[m][r];
+        sk[r] += xk[m][r] * xk[m][r];
+        pq[r] += xq[m][r] * dQa[m][r];
+        pk[r] += xk[m][r] * dKa[m][r];
       }
     }
 #pragma unroll
@@ -779,24 +893,36 @@ __global__ __launch_bounds__(256) void chunk_grad_kernel(
         pk[r] += __shfl_xor(pk[r], sh);
       }
     }
+    // combine the two column halves (RowP is free after the v-head loop)
+    if (r16 == 0) {
+      *reinterpret_cast<f32x4*>(&RowP[hf][0][row0]) = sq;
+      *reinterpret_cast<f32x4*>(&RowP[hf][1][row0]) = sk;
+      *reinterpret_cast<f32x4*>(&RowP[hf][2][row0]) = pq;
+      *reinterpret_cast<f32x4*>(&RowP[hf][3][row0]) = pk;
+    }
+    __syncthreads();
     // dx = r (dy - y (y . dy)), y = x r, r = (|x|^2 + eps)^-1/2
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float rq = rsqrtf(sq[r] + 1e-6f), rk2 = rsqrtf(sk[r] + 1e-6f);
+      const int i = row0 + r;
+      const float tq = RowP[0][0][i] + RowP[1][0][i], tk = RowP[0][1][i] + RowP[1][1][i];
+      const float uq = RowP[0][2][i] + RowP[1][2][i], uk = RowP[0][3][i] + RowP[1][3][i];
+      const float rq = rsqrtf(tq + 1e-6f), rk2 = rsqrtf(tk + 1e-6f);
 #pragma unroll
-      for (int ct = 0; ct < KT; ++ct) {
-        dQa[ct][r] = rq * (dQa[ct][r] - xq[ct][r] * rq * rq * pq[r]);
-        dKa[ct][r] = rk2 * (dKa[ct][r] - xk[ct][r] * rk2 * rk2 * pk[r]);
+      for (int m = 0; m < KH; ++m) {
+        dQa[m][r] = rq * (dQa[m][r] - xq[m][r] * rq * rq * uq);
+        dKa[m][r] = rk2 * (dKa[m][r] - xk[m][r] * rk2 * rk2 * uk);
       }
     }
   }
 #pragma unroll
-  for (int ct = 0; ct < KT; ++ct) {
+  for (int m = 0; m < KH; ++m) {
+    const int ct = 2 * m + hf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dQa[ct][r]), rdq, off, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dKa[ct][r]), rdk, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dQa[m][r]), rdq, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dKa[m][r]), rdk, off, 0, 0);
     }
   }
 }
@@ -822,7 +948,7 @@ static void launch_bwd_kernels(const uint16_t* q, const uint16_t* k, const uint1
   hipLaunchKernelGGL((chunk_rev_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, qn, kn,
                      dO, dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws);
   if (p.ncmax > 0)
-    hipLaunchKernelGGL((chunk_grad_kernel<K, V>), dim3((unsigned)p.ncmax, Hqk), dim3(256), 0,
+    hipLaunchKernelGGL((chunk_grad_kernel<K, V>), dim3((unsigned)p.ncmax, Hqk), dim3(kGradThreads), 0,
                        st, qn, kn, q, k, v, dO, beta, cu, N, T, total, Hqk, Hv, scale,
                        l2 ? 1 : 0, ws, dq, dk, dv, dg, dbeta);
 }

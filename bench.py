@@ -51,6 +51,20 @@ def prefill_flops(T, Hv, K=128, V=128):
     return (6 * C * K + 4 * C * V + 6 * K * V) * T * Hv
 
 
+def backward_flops(T, Hv, K=128, V=128):
+    """Flops of one gdn_chunk_bwd call: (16KV + 12CV + 18CK + 4C^2) per token per v-head.
+
+    Per chunk and v-head: the forward recomputation (K K^T, Q K^T in the prep;
+    K S, Tb Y, K^T U in the saving chain: 4CKV + 2C^2V + 4C^2K), the reverse
+    chain (K dS', P^T dO, Tb^T dd, K^T Z, Q^T dO: 6CKV + 4C^2V) and the
+    gradient kernel (dO S^T, dd S^T, d dS'^T: 6CKV; dO d^T, dd V^T, T^T dd:
+    6C^2V; R2 K^T, T^T dW, M K, M^T K, MP K, MP^T Q: 12C^2K; dT T^T and
+    T^T M1: 4C^3; K K^T and Q K^T once per qk-head: 2C^2K per v-head at G = 2).
+    hi/lo split passes are not counted.
+    """
+    return (16 * K * V + 12 * C * V + 18 * C * K + 4 * C * C) * T * Hv
+
+
 def decode_bytes(N, Hqk, Hv, K=128, V=128):
     """State read + write (fp32) plus q, k, v, o (bf16) and g, beta (fp32) per step."""
     return 2 * N * Hv * K * V * 4 + N * (2 * Hqk * K + 2 * Hv * V) * 2 + N * Hv * 2 * 4
@@ -111,6 +125,54 @@ def bench_prefill(dev, steps, warmup, l2norm=False):
     wall = time.perf_counter() - w0
     ms = e0.elapsed_time(e1) / steps
     return dict(ms=ms, wall_ms=wall * 1e3 / steps, T=T, Hv=Hv, K=K, V=V, wl=wl)
+
+
+def bench_backward(dev, steps, warmup):
+    """Graph replay of one gdn_chunk_bwd call at config 1 (dO ~ N(0,1) bf16, dht 0.01 N(0,1))."""
+    from avelang_amd import chunk_bwd_workspace_bytes, chunk_gated_delta_rule_bwd
+    from avelang_amd import workloads as W
+
+    wl = W.config("cfg1_prefill_qwen3next", seed=1)
+    d = wl.dims
+    t = wl.torch(dev)
+    B, T, Hqk, Hv, K, V, N = (d[x] for x in ("B", "T", "Hqk", "Hv", "K", "V", "N"))
+    gen = torch.Generator(device=dev).manual_seed(11)
+    do = torch.randn((B, T, Hv, V), generator=gen, device=dev).to(torch.bfloat16)
+    dht = 0.01 * torch.randn((N, Hv, K, V), generator=gen, device=dev)
+    ws = torch.empty(chunk_bwd_workspace_bytes(B, T, Hqk, Hv, K, V, N, False),
+                     dtype=torch.uint8, device=dev)
+
+    def call():
+        chunk_gated_delta_rule_bwd(t["q"], t["k"], t["v"], t["g"], t["beta"], do, dht,
+                                   initial_state=t["initial_state"], workspace=ws)
+
+    ms = _time_graph(dev, call, launches=max(steps // 5, 1), reps=5)
+    return dict(ms=ms, T=T, Hv=Hv, K=K, V=V, wl=wl, ws_bytes=ws.numel())
+
+
+def cpu_backward(wl, heads=4):
+    """The fp32 numpy chunked backward oracle on config 1 restricted to ``heads`` v-heads."""
+    from threadpoolctl import threadpool_info
+
+    from oracle import gdn_bwd_ref as RB
+
+    a = wl.numpy()
+    hq = heads // 2
+    rng = np.random.Generator(np.random.PCG64(5))
+    T = wl.dims["T"]
+    do = rng.standard_normal((1, T, heads, wl.dims["V"]), dtype=np.float32)
+    sub = dict(q=a["q"][:, :, :hq], k=a["k"][:, :, :hq], v=a["v"][:, :, :heads],
+               g=a["g"][:, :, :heads], beta=a["beta"][:, :, :heads],
+               initial_state=a["initial_state"][:, :heads])
+    t0 = time.perf_counter()
+    RB.chunked_bwd(sub["q"], sub["k"], sub["v"], sub["g"], sub["beta"], do, None,
+                   initial_state=sub["initial_state"], dtype=np.float32)
+    dt = time.perf_counter() - t0
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    full = dt * wl.dims["Hv"] / heads
+    return dict(value=T / full, unit="tokens/s", cores=threads, kind="port",
+                sample=f"config 1 with {heads} of 32 v-heads (T={T}), numpy fp32 chunked "
+                       f"backward oracle, {dt:.1f} s, scaled to 32 heads")
 
 
 def bench_prefill_config(dev, name, reps=3):
@@ -358,6 +420,26 @@ def profile_pass(dev, reps=3):
     print("profile pass done", flush=True)
 
 
+def _backward_record(bwd, no_cpu):
+    flops = backward_flops(bwd["T"], bwd["Hv"], bwd["K"], bwd["V"])
+    tf = flops / (bwd["ms"] * 1e-3) / 1e12
+    return {
+        "workload": "cfg1 chunk_gated_delta_rule backward (gdn_chunk_bwd: forward recompute, "
+                    "reverse state-gradient chain, per-chunk gradients)",
+        "value": round(bwd["T"] / (bwd["ms"] * 1e-3), 1), "unit": "tokens/s",
+        "ms_per_step": round(bwd["ms"], 5),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                     "traffic": _load_traffic("backward"),
+                     "kernel": "gdn_chunk_bwd = chunk_prep<bwd> + chunk_chain<save> + "
+                               "chunk_rev + chunk_grad",
+                     "algorithmic_flops_per_launch": flops,
+                     "flops_per_token_per_vhead": flops // (bwd["T"] * bwd["Hv"])},
+        "workspace_bytes": bwd["ws_bytes"],
+        "cpu_baseline": None if no_cpu else cpu_backward(bwd["wl"]),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -391,6 +473,7 @@ def main():
     pre_l2 = bench_prefill(dev, max(args.steps // 2, 1), args.warmup, l2norm=True) if extra else None
     others = ([bench_prefill_config(dev, n) for n in ("cfg3_varlen_64seq", "cfg4_long_context")]
               if extra else None)
+    bwd = bench_backward(dev, args.steps, args.warmup) if extra else None
 
     flops = prefill_flops(pre["T"], pre["Hv"], pre["K"], pre["V"])
     tflops = flops / (pre["ms"] * 1e-3) / 1e12
@@ -441,6 +524,7 @@ def main():
             "value": round(pre_l2["T"] / (pre_l2["ms"] * 1e-3), 1), "unit": "tokens/s",
             "ms_per_step": round(pre_l2["ms"], 5)},
         "prefill_other_configs": others,
+        "backward": None if bwd is None else _backward_record(bwd, args.no_cpu),
         "layer_ops": layer,
         "host_wall_ms_per_step": round(pre["wall_ms"], 5),
     }
