@@ -17,6 +17,7 @@ from .gated_delta_rule import (  # noqa: F401
     chunk_bwd_workspace_bytes,
     chunk_gated_delta_rule,
     chunk_gated_delta_rule_bwd,
+    chunk_gated_delta_rule_fwd_save,
     chunk_workspace_bytes,
     fused_recurrent_gated_delta_rule,
 )
@@ -31,6 +32,7 @@ from .layer_ops import (  # noqa: F401
 __all__ = [
     "chunk_gated_delta_rule",
     "chunk_gated_delta_rule_bwd",
+    "chunk_gated_delta_rule_fwd_save",
     "fused_recurrent_gated_delta_rule",
     "chunk_workspace_bytes",
     "chunk_bwd_workspace_bytes",

@@ -19,6 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libgdn.so"
 EXPORTS = (
     "gdn_chunk_fwd",
     "gdn_chunk_workspace_bytes",
+    "gdn_chunk_fwd_save",
     "gdn_chunk_bwd",
     "gdn_chunk_bwd_workspace_bytes",
     "gdn_recurrent_fwd",
@@ -83,6 +84,8 @@ def lib():
         ]
         h.gdn_chunk_workspace_bytes.restype = _sz
         h.gdn_chunk_workspace_bytes.argtypes = [_i] * 9
+        h.gdn_chunk_fwd_save.restype = _i
+        h.gdn_chunk_fwd_save.argtypes = h.gdn_chunk_fwd.argtypes
         h.gdn_chunk_bwd.restype = _i
         h.gdn_chunk_bwd.argtypes = [
             _vp, _vp, _vp, _vp, _vp, _vp,     # q k v g beta h0
@@ -90,7 +93,7 @@ def lib():
             _vp, _vp, _vp, _vp, _vp, _vp,     # dq dk dv dg dbeta dh0
             _vp,                              # cu_seqlens
             _i, _i, _i, _i, _i, _i, _i,       # B T Hqk Hv K V N
-            _f, _i, _vp, _sz, _vp,            # scale l2norm ws ws_bytes stream
+            _f, _i, _i, _vp, _sz, _vp,        # scale l2norm saved ws ws_bytes stream
         ]
         h.gdn_chunk_bwd_workspace_bytes.restype = _sz
         h.gdn_chunk_bwd_workspace_bytes.argtypes = [_i] * 9

@@ -71,13 +71,16 @@ struct WsPlan {
 WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, bool l2,
                bool bwd);
 
-// Enqueue the chunk table, the prep and the forward chain.  With `bwd` the
-// prep also writes tmat / ttfrag / ptfrag and the chain saves hs / dl
-// instead of writing o (o and ht are then ignored).
+// What a forward launch sequence writes: kForward = o / ht only; kRecompute =
+// the backward's inputs only (prep adds tmat / ttfrag / ptfrag, the chain
+// saves hs / dl; o and ht are ignored); kSave = both (a training forward).
+enum class FwdMode { kForward, kRecompute, kSave };
+
+// Enqueue the chunk table, the prep and the forward chain.
 void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                       const float* beta, const float* h0, float* ht, uint16_t* o,
                       const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N,
-                      float scale, bool l2, bool bwd, const WsPlan& p, unsigned char* wsb,
+                      float scale, bool l2, FwdMode mode, const WsPlan& p, unsigned char* wsb,
                       hipStream_t st);
 
 ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb);

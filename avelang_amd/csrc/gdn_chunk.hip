@@ -467,9 +467,11 @@ __device__ __forceinline__ void chain_load_c(ChainIn<K>& in, const ChainCtx& c, 
   in.G = c.ws.gate[((size_t)ci * c.Hv + c.h) * 64 + c.lane];
 }
 
-// SAVE (the backward's recomputation): store the state at every chunk start
-// (ws.hs) and the per-token delta (ws.dl) instead of writing o.
-template <int K, bool SAVE>
+// SAVE: store the state at every chunk start (ws.hs) and the per-token delta
+// (ws.dl) for the backward.  OUT: write o (and ht when given).  The forward
+// is <K, false, true>, the backward's recomputation <K, true, false>, a
+// training forward that keeps what the backward needs <K, true, true>.
+template <int K, bool SAVE, bool OUT>
 __global__ __launch_bounds__(256) void chunk_chain_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
@@ -662,9 +664,8 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
         for (int r = 0; r < 4; ++r)
           __builtin_amdgcn_raw_buffer_store_b16(
               vb[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
-      } else {
-        *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
       }
+      if constexpr (OUT) *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
     }
     __syncthreads();
     chain_load_c<K>(nxt, ctx, cn);
@@ -689,7 +690,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     }
     // o^T = scale e^G (Q S)^T + vnew^T P^T: lane holds row 16w + r16,
     // columns 16 vt + 4 grp .. + 3
-    if constexpr (!SAVE) {
+    if constexpr (OUT) {
       const u16x8 v0 = *reinterpret_cast<const u16x8*>(&VnT[r16][8 * grp]);
       const u16x8 v1 = *reinterpret_cast<const u16x8*>(&VnT[r16][32 + 8 * grp]);
       const f32x4 oa = mfma16(v0, cur.pf[0], zero4());
@@ -796,7 +797,7 @@ ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb) {
   return ws;
 }
 
-template <int K, bool BWD>
+template <int K, bool BWD, bool OUT>
 static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                          const float* g, const float* beta, const float* h0, float* ht,
                          uint16_t* o, const int32_t* cu, int B, int T, int Hqk, int Hv, int V,
@@ -811,31 +812,29 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
     hipLaunchKernelGGL((chunk_prep_kernel<K, BWD>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0,
                        st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised
-  hipLaunchKernelGGL((chunk_chain_kernel<K, BWD>), dim3(N * Hv * (V / 16)), dim3(256), 0, st,
-                     l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, BWD ? nullptr : ht,
-                     BWD ? nullptr : o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  hipLaunchKernelGGL((chunk_chain_kernel<K, BWD, OUT>), dim3(N * Hv * (V / 16)), dim3(256), 0, st,
+                     l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
+                     OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws);
 }
 
 void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                       const float* beta, const float* h0, float* ht, uint16_t* o,
                       const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N,
-                      float scale, bool l2, bool bwd, const WsPlan& p, unsigned char* wsb,
+                      float scale, bool l2, FwdMode mode, const WsPlan& p, unsigned char* wsb,
                       hipStream_t st) {
+#define GDN_FWD(KK_, BWD_, OUT_)                                                             \
+  launch_chunk<KK_, BWD_, OUT_>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2, \
+                                p, wsb, st)
   if (K == 128) {
-    if (bwd)
-      launch_chunk<128, true>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2,
-                              p, wsb, st);
-    else
-      launch_chunk<128, false>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2,
-                               p, wsb, st);
+    if (mode == FwdMode::kForward) GDN_FWD(128, false, true);
+    else if (mode == FwdMode::kRecompute) GDN_FWD(128, true, false);
+    else GDN_FWD(128, true, true);
   } else {
-    if (bwd)
-      launch_chunk<64, true>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2, p,
-                             wsb, st);
-    else
-      launch_chunk<64, false>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2,
-                              p, wsb, st);
+    if (mode == FwdMode::kForward) GDN_FWD(64, false, true);
+    else if (mode == FwdMode::kRecompute) GDN_FWD(64, true, false);
+    else GDN_FWD(64, true, true);
   }
+#undef GDN_FWD
 }
 
 }  // namespace gdn
@@ -873,7 +872,33 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
   gdn::launch_chunk_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                         static_cast<const uint16_t*>(v), g, beta, h0, ht,
                         static_cast<uint16_t*>(o), cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
-                        use_qk_l2norm != 0, false, p, static_cast<unsigned char*>(workspace),
+                        use_qk_l2norm != 0, gdn::FwdMode::kForward, p,
+                        static_cast<unsigned char*>(workspace),
                         static_cast<hipStream_t>(stream));
   return gdn_host::check_launch("gdn_chunk_fwd");
+}
+
+extern "C" int gdn_chunk_fwd_save(const void* q, const void* k, const void* v, const float* g,
+                                  const float* beta, const float* h0, float* ht, void* o,
+                                  const int32_t* cu_seqlens, int B, int T, int Hqk, int Hv, int K,
+                                  int V, int N, float scale, int use_qk_l2norm, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk, Hv,
+                                     K, V, N);
+  if (rc) return rc;
+  if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
+  const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
+                                     use_qk_l2norm != 0, true);
+  if (!workspace || workspace_bytes < p.total)
+    return gdn_host::fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd_save: workspace needs " +
+                                                 std::to_string(p.total) + " bytes, got " +
+                                                 std::to_string(workspace_bytes));
+  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_fwd_save: problem too large");
+  gdn::launch_chunk_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                        static_cast<const uint16_t*>(v), g, beta, h0, ht,
+                        static_cast<uint16_t*>(o), cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
+                        use_qk_l2norm != 0, gdn::FwdMode::kSave, p,
+                        static_cast<unsigned char*>(workspace), static_cast<hipStream_t>(stream));
+  return gdn_host::check_launch("gdn_chunk_fwd_save");
 }

@@ -402,7 +402,6 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   __shared__ __attribute__((aligned(16))) float Bs[64];
   __shared__ __attribute__((aligned(16))) float Cs[64];     // column sums of X
   __shared__ __attribute__((aligned(16))) float Cv[64];     // column sums of T * (dd V^T)
-  __shared__ __attribute__((aligned(16))) float Ds[64];     // dG per row
   __shared__ __attribute__((aligned(16))) float RowP[2][5][64];   // row partials per half
   __shared__ float Red[8];
 
@@ -434,7 +433,6 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   const int w8 = __builtin_amdgcn_readfirstlane(tid / 64);   // wave index (scalar)
   const int rt = w8 & 3, hf = w8 >> 2;
   const int r16 = lane % 16, grp = lane / 16;
-  const int rowA = 16 * rt + r16;         // A-fragment row of this lane
   const int row0 = 16 * rt + 4 * grp;     // first OL row of this lane
 
   // K / Q rows of the chunk (rows >= L read as zero)
@@ -973,8 +971,8 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
                              const float* dht, void* dq, void* dk, void* dv, float* dg,
                              float* dbeta, float* dh0, const int32_t* cu_seqlens, int B, int T,
                              int Hqk, int Hv, int K, int V, int N, float scale,
-                             int use_qk_l2norm, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+                             int use_qk_l2norm, int saved, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   int rc = gdn_host::validate_common(q, k, v, g, beta, h0, nullptr, dO, cu_seqlens, B, T, Hqk,
                                      Hv, K, V, N);
   if (rc) return rc;
@@ -997,9 +995,11 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   auto* vv = static_cast<const uint16_t*>(v);
   const bool l2 = use_qk_l2norm != 0;
   // forward recomputation: prep (with T, Tb^T, P^T) and the chain saving the
-  // chunk-start states and the deltas
-  gdn::launch_chunk_fwd(qq, kk, vv, g, beta, h0, nullptr, nullptr, cu_seqlens, B, T, Hqk, Hv,
-                        K, V, N, scale, l2, true, p, wsb, st);
+  // chunk-start states and the deltas -- unless gdn_chunk_fwd_save already
+  // left them in this workspace
+  if (!saved)
+    gdn::launch_chunk_fwd(qq, kk, vv, g, beta, h0, nullptr, nullptr, cu_seqlens, B, T, Hqk, Hv,
+                          K, V, N, scale, l2, gdn::FwdMode::kRecompute, p, wsb, st);
   const uint16_t* qn = l2 ? reinterpret_cast<const uint16_t*>(wsb + p.qn) : qq;
   const uint16_t* kn = l2 ? reinterpret_cast<const uint16_t*>(wsb + p.kn) : kk;
   auto* ddo = static_cast<const uint16_t*>(dO);

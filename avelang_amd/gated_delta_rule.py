@@ -27,6 +27,7 @@ from . import _native
 __all__ = [
     "chunk_gated_delta_rule",
     "chunk_gated_delta_rule_bwd",
+    "chunk_gated_delta_rule_fwd_save",
     "fused_recurrent_gated_delta_rule",
     "chunk_workspace_bytes",
     "chunk_bwd_workspace_bytes",
@@ -138,6 +139,7 @@ def chunk_gated_delta_rule_bwd(
     use_qk_l2norm_in_kernel: bool = False,
     *,
     workspace: Optional[torch.Tensor] = None,
+    saved: bool = False,
 ):
     """Gradients of ``chunk_gated_delta_rule`` (gdn_chunk_bwd).
 
@@ -145,8 +147,11 @@ def chunk_gated_delta_rule_bwd(
     state).  Returns ``(dq, dk, dv, dg, dbeta, dh0)``: dq, dk, dv in bf16,
     dg, dbeta in fp32, dh0 fp32 (``None`` without ``initial_state``).  The
     forward is recomputed from the inputs; nothing is kept from the forward
-    call.  With ``use_qk_l2norm_in_kernel`` dq and dk are gradients with
-    respect to the raw q and k.
+    call -- unless ``saved``: then ``workspace`` must be the one a training
+    forward (``chunk_gated_delta_rule_fwd_save``) filled for these same
+    inputs, and the recomputation is skipped.  With
+    ``use_qk_l2norm_in_kernel`` dq and dk are gradients with respect to the
+    raw q and k.
     """
     name = "chunk_gated_delta_rule_bwd"
     q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
@@ -173,6 +178,8 @@ def chunk_gated_delta_rule_bwd(
     nbytes = chunk_bwd_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu is not None,
                                        use_qk_l2norm_in_kernel)
     if workspace is None:
+        if saved:
+            raise ValueError(f"{name}: saved=True needs the training forward's workspace.")
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     elif workspace.numel() * workspace.element_size() < nbytes or workspace.device != dev:
         raise ValueError(f"{name}: workspace must be >= {nbytes} bytes on {dev}.")
@@ -181,20 +188,70 @@ def chunk_gated_delta_rule_bwd(
         do.data_ptr(), _ptr(dht),
         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), dbeta.data_ptr(), _ptr(dh0),
         _ptr(cu), B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
-        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream_ptr(dev))
+        int(bool(saved)), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        _stream_ptr(dev))
     _native.check(rc, name)
     return dq, dk, dv, dg, dbeta, dh0
 
 
+def chunk_gated_delta_rule_fwd_save(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    *,
+    workspace: Optional[torch.Tensor] = None,
+):
+    """Training forward (gdn_chunk_fwd_save): ``(o, final_state, workspace)``.
+
+    ``o`` and ``final_state`` equal ``chunk_gated_delta_rule``'s; the
+    returned workspace (``chunk_bwd_workspace_bytes`` bytes) holds what
+    ``chunk_gated_delta_rule_bwd(..., workspace=ws, saved=True)`` needs for
+    these same inputs.
+    """
+    if workspace is None:
+        B, T, Hqk, K = q.shape
+        Hv, V = v.shape[2], v.shape[3]
+        N = B if cu_seqlens is None else cu_seqlens.numel() - 1
+        nbytes = chunk_bwd_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu_seqlens is not None,
+                                           use_qk_l2norm_in_kernel)
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    o, ht = _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
+                       use_qk_l2norm_in_kernel, save_workspace=workspace)
+    return o, ht, workspace
+
+
+# The autograd forward keeps the backward's workspace (chunk-start states,
+# deltas, the prep's fragments: ~82 KB per chunk and v-head, 672 MB for a
+# T = 8192, 32-head layer) alive until the backward, which then skips the
+# forward recomputation.  False: keep only the inputs and recompute.
+SAVE_FORWARD_FOR_BACKWARD = True
+
+
 class _ChunkGatedDeltaRule(torch.autograd.Function):
-    """Autograd form of chunk_gated_delta_rule: forward gdn_chunk_fwd,
-    backward gdn_chunk_bwd (the forward is recomputed, only inputs saved)."""
+    """Autograd form of chunk_gated_delta_rule: forward gdn_chunk_fwd_save
+    (or gdn_chunk_fwd), backward gdn_chunk_bwd (saved = 1, or recomputing)."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
                 use_qk_l2norm_in_kernel):
+        ws = None
+        if SAVE_FORWARD_FOR_BACKWARD:
+            B, T, Hqk, K = q.shape
+            Hv, V = v.shape[2], v.shape[3]
+            N = B if cu_seqlens is None else cu_seqlens.numel() - 1
+            nbytes = chunk_bwd_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu_seqlens is not None,
+                                               use_qk_l2norm_in_kernel)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         o, ht = _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state,
-                           cu_seqlens, use_qk_l2norm_in_kernel)
+                           cu_seqlens, use_qk_l2norm_in_kernel, save_workspace=ws)
+        ctx.ws = ws
         ctx.save_for_backward(q, k, v, g, beta, initial_state, cu_seqlens)
         ctx.scale = scale
         ctx.l2 = use_qk_l2norm_in_kernel
@@ -209,9 +266,10 @@ class _ChunkGatedDeltaRule(torch.autograd.Function):
         q, k, v, g, beta, h0, cu = ctx.saved_tensors
         if dht is not None and not ctx.has_ht:
             dht = None
+        ws, ctx.ws = ctx.ws, None
         dq, dk, dv, dg, db, dh0 = chunk_gated_delta_rule_bwd(
             q, k, v, g, beta, do.to(torch.bfloat16), dht.float() if dht is not None else None,
-            ctx.scale, h0, cu, ctx.l2)
+            ctx.scale, h0, cu, ctx.l2, workspace=ws, saved=ws is not None)
         return (dq, dk, dv, dg.to(ctx.g_dtype), db.to(ctx.beta_dtype), None, dh0, None, None,
                 None)
 
@@ -263,7 +321,10 @@ def chunk_gated_delta_rule(
 
 
 def _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
-               use_qk_l2norm_in_kernel, workspace=None, out=None, final_state=None):
+               use_qk_l2norm_in_kernel, workspace=None, out=None, final_state=None,
+               save_workspace=None):
+    """gdn_chunk_fwd, or gdn_chunk_fwd_save into ``save_workspace`` (a
+    backward-sized workspace the backward then reuses)."""
     name = "chunk_gated_delta_rule"
     q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
         q, k, v, g, beta, initial_state, cu_seqlens, name)
@@ -283,12 +344,19 @@ def _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_se
             if (tuple(ht.shape) != (N, Hv, K, V) or ht.dtype != torch.float32
                     or ht.device != dev or not ht.is_contiguous()):
                 raise ValueError(f"{name}: final_state must be contiguous fp32 {(N, Hv, K, V)}.")
-    nbytes = chunk_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu is not None, use_qk_l2norm_in_kernel)
+    entry = _native.lib().gdn_chunk_fwd
+    if save_workspace is not None:
+        workspace, entry = save_workspace, _native.lib().gdn_chunk_fwd_save
+        nbytes = chunk_bwd_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu is not None,
+                                           use_qk_l2norm_in_kernel)
+    else:
+        nbytes = chunk_workspace_bytes(B, T, Hqk, Hv, K, V, N, cu is not None,
+                                       use_qk_l2norm_in_kernel)
     if workspace is None:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     elif workspace.numel() * workspace.element_size() < nbytes or workspace.device != dev:
         raise ValueError(f"{name}: workspace must be >= {nbytes} bytes on {dev}.")
-    rc = _native.lib().gdn_chunk_fwd(
+    rc = entry(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
         _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
         B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),

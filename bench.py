@@ -146,8 +146,28 @@ def bench_backward(dev, steps, warmup):
         chunk_gated_delta_rule_bwd(t["q"], t["k"], t["v"], t["g"], t["beta"], do, dht,
                                    initial_state=t["initial_state"], workspace=ws)
 
-    ms = _time_graph(dev, call, launches=max(steps // 5, 1), reps=5)
-    return dict(ms=ms, T=T, Hv=Hv, K=K, V=V, wl=wl, ws_bytes=ws.numel())
+    launches = max(steps // 5, 1)
+    ms = _time_graph(dev, call, launches=launches, reps=5)
+
+    # training step: the forward that keeps the backward's inputs, and the
+    # backward from that workspace (no recomputation)
+    from avelang_amd import chunk_gated_delta_rule_fwd_save
+    o = torch.empty_like(t["v"])
+
+    def fwd_save():
+        chunk_gated_delta_rule_fwd_save(t["q"], t["k"], t["v"], t["g"], t["beta"],
+                                        initial_state=t["initial_state"],
+                                        output_final_state=True, workspace=ws)
+
+    def bwd_saved():
+        chunk_gated_delta_rule_bwd(t["q"], t["k"], t["v"], t["g"], t["beta"], do, dht,
+                                   initial_state=t["initial_state"], workspace=ws, saved=True)
+
+    ms_fs = _time_graph(dev, fwd_save, launches=launches, reps=5)
+    fwd_save()
+    ms_bs = _time_graph(dev, bwd_saved, launches=launches, reps=5)
+    return dict(ms=ms, ms_fwd_save=ms_fs, ms_bwd_saved=ms_bs, T=T, Hv=Hv, K=K, V=V, wl=wl,
+                ws_bytes=ws.numel())
 
 
 def cpu_backward(wl, heads=4):
@@ -436,6 +456,12 @@ def _backward_record(bwd, no_cpu):
                      "algorithmic_flops_per_launch": flops,
                      "flops_per_token_per_vhead": flops // (bwd["T"] * bwd["Hv"])},
         "workspace_bytes": bwd["ws_bytes"],
+        "training_step": {
+            "what": "autograd path: forward keeping the backward's inputs (gdn_chunk_fwd_save) "
+                    "+ backward from that workspace (gdn_chunk_bwd saved=1)",
+            "fwd_ms": round(bwd["ms_fwd_save"], 5), "bwd_ms": round(bwd["ms_bwd_saved"], 5),
+            "value": round(bwd["T"] / ((bwd["ms_fwd_save"] + bwd["ms_bwd_saved"]) * 1e-3), 1),
+            "unit": "tokens/s (forward + backward)"},
         "cpu_baseline": None if no_cpu else cpu_backward(bwd["wl"]),
     }
 

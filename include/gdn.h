@@ -76,6 +76,23 @@ size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
                                  int N, int has_cu_seqlens, int use_qk_l2norm);
 
 /*
+ * Training forward: gdn_chunk_fwd's results (o, ht) plus, in `workspace`
+ * (at least gdn_chunk_bwd_workspace_bytes(...)), everything gdn_chunk_bwd
+ * needs, so that a later gdn_chunk_bwd(..., saved = 1, same workspace) on
+ * the same inputs skips its forward recomputation.  The forward half of an
+ * autograd chunk_gated_delta_rule (FLA's autograd function; Qwen3-Next trains
+ * through it, modeling_qwen3_next.py:672-683); no reference counterpart.
+ */
+int gdn_chunk_fwd_save(const void* q, const void* k, const void* v,
+                       const float* g, const float* beta,
+                       const float* h0, float* ht, void* o,
+                       const int32_t* cu_seqlens,
+                       int B, int T, int Hqk, int Hv, int K, int V, int N,
+                       float scale, int use_qk_l2norm,
+                       void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
  * Fused recurrent form (decode: T == 1 per sequence; also multi-token).
  * Replaces the launcher call of `fused_recurrent_gated_delta_rule`
  * (semantics modeling_qwen3_next.py:456-503).  The state tile of each
@@ -101,9 +118,10 @@ int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
  * reference repository has no counterpart (its kernel library,
  * python/avelang_kernels/, is forward-only and holds one GEMM).
  *
- * Recomputes the forward from (q, k, v, g, beta, h0) -- nothing has to be
- * kept from the forward call -- then runs the state gradient backwards over
- * the chunks and forms every chunk's local gradients in parallel.
+ * Recomputes the forward from (q, k, v, g, beta, h0) -- or takes it from a
+ * gdn_chunk_fwd_save workspace (saved != 0) -- then runs the state gradient
+ * backwards over the chunks and forms every chunk's local gradients in
+ * parallel.
  *
  *   dO    [B, T, Hv, V] bf16: dL/do.
  *   dht   nullable: dL/d(final state) [N, Hv, K, V] fp32; NULL = zeros.
@@ -113,6 +131,9 @@ int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
  *         the gradient with respect to a zero initial state).
  *   use_qk_l2norm != 0: the forward normalised q and k; dq and dk are the
  *         gradients with respect to the raw (unnormalised) q and k.
+ *   saved != 0: `workspace` holds what gdn_chunk_fwd_save left there for
+ *         these same inputs; the forward recomputation is skipped.  0: the
+ *         forward is recomputed from (q, k, v, g, beta, h0).
  *   workspace: at least gdn_chunk_bwd_workspace_bytes(...).
  * Every output is fully overwritten (no accumulation into it).
  */
@@ -122,11 +143,11 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v,
                   void* dq, void* dk, void* dv, float* dg, float* dbeta, float* dh0,
                   const int32_t* cu_seqlens,
                   int B, int T, int Hqk, int Hv, int K, int V, int N,
-                  float scale, int use_qk_l2norm,
+                  float scale, int use_qk_l2norm, int saved,
                   void* workspace, size_t workspace_bytes,
                   void* stream);
 
-/* Bytes of device workspace gdn_chunk_bwd needs for these sizes. */
+/* Bytes of device workspace gdn_chunk_bwd (and gdn_chunk_fwd_save) need. */
 size_t gdn_chunk_bwd_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
                                      int N, int has_cu_seqlens, int use_qk_l2norm);
 

@@ -28,8 +28,8 @@ def _declared(headers=("gdn.h", "gdn_layer.h")):
 def test_header_declares_expected_entry_points():
     assert _declared(("gdn.h",)) == ["gdn_abi_version", "gdn_chunk_bwd",
                                      "gdn_chunk_bwd_workspace_bytes", "gdn_chunk_fwd",
-                                     "gdn_chunk_workspace_bytes", "gdn_last_error",
-                                     "gdn_recurrent_fwd"]
+                                     "gdn_chunk_fwd_save", "gdn_chunk_workspace_bytes",
+                                     "gdn_last_error", "gdn_recurrent_fwd"]
     assert _declared(("gdn_layer.h",)) == [
         "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_gating_fwd",
         "gdn_l2norm_fwd", "gdn_recurrent_fwd_indexed", "gdn_rmsnorm_gated_fwd"]

@@ -180,3 +180,61 @@ def test_bwd_deterministic(rocm_device):
     b = _gpu_bwd(wl, do, dht, rocm_device)
     for key in a:
         assert torch.equal(a[key], b[key]), key
+
+
+def test_training_forward_matches_forward(rocm_device):
+    """gdn_chunk_fwd_save gives gdn_chunk_fwd's o and final state, bitwise."""
+    from avelang_amd import chunk_gated_delta_rule, chunk_gated_delta_rule_fwd_save
+    cu = np.array([0, 70, 71, 230], dtype=np.int32)
+    for l2 in (False, True):
+        wl = W.make(1, 230, 2, 4, 128, 128, seed=40, cu_seqlens=cu, l2norm=not l2)
+        t = wl.torch(rocm_device)
+        kw = dict(initial_state=t["initial_state"], output_final_state=True,
+                  cu_seqlens=t["cu_seqlens"], use_qk_l2norm_in_kernel=l2)
+        o1, s1 = chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"], **kw)
+        o2, s2, _ = chunk_gated_delta_rule_fwd_save(t["q"], t["k"], t["v"], t["g"], t["beta"],
+                                                    **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and torch.equal(s1, s2), f"l2norm={l2}"
+
+
+@pytest.mark.parametrize("l2", [False, True])
+def test_saved_backward_equals_recomputed(rocm_device, l2):
+    """The backward from a training forward's workspace == the recomputing backward."""
+    from avelang_amd import chunk_gated_delta_rule_bwd, chunk_gated_delta_rule_fwd_save
+    cu = np.array([0, 0, 100, 163, 300], dtype=np.int32)
+    wl = W.make(1, 300, 2, 4, 128, 128, seed=41, cu_seqlens=cu, l2norm=not l2)
+    do, dht = _grad_inputs(wl, 41)
+    t = wl.torch(rocm_device)
+    _, _, ws = chunk_gated_delta_rule_fwd_save(
+        t["q"], t["k"], t["v"], t["g"], t["beta"], initial_state=t["initial_state"],
+        output_final_state=True, cu_seqlens=t["cu_seqlens"], use_qk_l2norm_in_kernel=l2)
+    args = (t["q"], t["k"], t["v"], t["g"], t["beta"],
+            torch.from_numpy(do).to(device=rocm_device, dtype=torch.bfloat16),
+            torch.from_numpy(dht).to(rocm_device))
+    kw = dict(initial_state=t["initial_state"], cu_seqlens=t["cu_seqlens"],
+              use_qk_l2norm_in_kernel=l2)
+    a = chunk_gated_delta_rule_bwd(*args, workspace=ws, saved=True, **kw)
+    b = chunk_gated_delta_rule_bwd(*args, **kw)
+    torch.cuda.synchronize()
+    for name, x, y in zip(("dq", "dk", "dv", "dg", "dbeta", "dh0"), a, b):
+        assert torch.equal(x, y), name
+
+
+def test_autograd_without_saved_forward(rocm_device, monkeypatch):
+    """SAVE_FORWARD_FOR_BACKWARD = False (recompute) gives the same gradients."""
+    from avelang_amd import chunk_gated_delta_rule
+    from avelang_amd import gated_delta_rule as GDR
+    wl = W.make(1, 150, 2, 4, 128, 128, seed=42)
+    do, _ = _grad_inputs(wl, 42)
+    dO = torch.from_numpy(do).to(device=rocm_device, dtype=torch.bfloat16)
+    grads = []
+    for flag in (True, False):
+        monkeypatch.setattr(GDR, "SAVE_FORWARD_FOR_BACKWARD", flag)
+        t = wl.torch(rocm_device)
+        leaves = [t[n].clone().requires_grad_(True) for n in ("q", "k", "v", "g", "beta")]
+        o, _ = chunk_gated_delta_rule(*leaves, initial_state=t["initial_state"])
+        (o.float() * dO.float()).sum().backward()
+        grads.append([x.grad for x in leaves])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
