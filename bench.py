@@ -395,7 +395,8 @@ def profile_pass(dev, reps=3):
        WRITE_SIZE against known bytes: 256 MiB read, 256 MiB written);
     2. ``reps`` config-1 prefill calls (chunk_prep, chunk_chain);
     3. ``reps`` config-2 decode steps (recurrent_kernel<128,128>);
-    4. ``reps`` calls of each layer operator at the Qwen3-Next layer shape.
+    4. ``reps`` calls of each layer operator at the Qwen3-Next layer shape;
+    5. ``reps`` config-1 backward calls (gdn_chunk_bwd with its recomputation).
     """
     from avelang_amd import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule
     from avelang_amd import workloads as W
@@ -437,7 +438,67 @@ def profile_pass(dev, reps=3):
         L.l2norm_fwd(qk)
         L.rms_norm_gated(o, o, nw)
     torch.cuda.synchronize(dev)
+    from avelang_amd import chunk_gated_delta_rule_bwd
+    do = torch.randn((1, T, Hv, K), device=dev).to(torch.bfloat16)
+    for _ in range(reps):
+        chunk_gated_delta_rule_bwd(t["q"], t["k"], t["v"], t["g"], t["beta"], do, None,
+                                   initial_state=t["initial_state"])
+    torch.cuda.synchronize(dev)
     print("profile pass done", flush=True)
+
+
+def pmc_summary(fetch_dir, write_dir, out_path):
+    """profiles/traffic.json from two rocprofv3 --pmc runs of --profile-pass.
+
+    Each counter is averaged per kernel over its dispatches and scaled by
+    what it reads for the pass's 256 MiB device copy (known bytes), so the
+    figures are HBM bytes per launch.  Path totals: prefill = chunk_prep +
+    chunk_chain (forward instantiations), backward = the four launches of
+    gdn_chunk_bwd, decode = the recurrent kernel.
+    """
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        acc = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                name = r["Kernel_Name"].split("(")[0].replace("void ", "").strip()
+                disp = (r.get("Dispatch_Id") or r.get("Correlation_Id"))
+                acc.setdefault(name, {}).setdefault(disp, 0.0)
+                acc[name][disp] += float(r["Counter_Value"])   # summed over dimensions
+        return {k: float(np.mean(list(v.values()))) * 1024 for k, v in acc.items()}  # KiB -> B
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    copy = [k for k in fetch if "copyBuffer" in k]
+    if not copy:
+        raise SystemExit("pmc_summary: the calibration copy is missing")
+    ff = (256 << 20) / fetch[copy[0]]
+    wf = (256 << 20) / write[copy[0]]
+    kern = {k: {"fetch_bytes": int(fetch[k] * ff), "write_bytes": int(write.get(k, 0) * wf)}
+            for k in sorted(fetch) if k.startswith("gdn::")}
+
+    def total(pred):
+        return sum(v["fetch_bytes"] + v["write_bytes"] for k, v in kern.items() if pred(k))
+
+    res = {
+        "prefill": total(lambda k: ("chunk_prep_kernel<128, false>" in k
+                                    or "chunk_chain_kernel<128, false, true>" in k)),
+        "decode": total(lambda k: "recurrent_kernel<128, 128" in k),
+        "backward": total(lambda k: ("chunk_prep_kernel<128, true>" in k
+                                     or "chunk_chain_kernel<128, true, false>" in k
+                                     or "chunk_rev_kernel<128>" in k
+                                     or "chunk_grad_kernel<128, 128>" in k)),
+        "per_kernel": kern,
+        "fetch_size_factor": round(ff, 4),
+        "write_size_factor": round(wf, 4),
+        "calibration": "one 256 MiB device-to-device copy in the same run",
+    }
+    with open(out_path, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps({k: res[k] for k in ("prefill", "decode", "backward")}))
 
 
 def _backward_record(bwd, no_cpu):
@@ -479,7 +540,15 @@ def main():
                     help="only the config-1 prefill and config-2 decode lines (profiling runs)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run the fixed untimed launch sequence used for rocprofv3 --pmc runs")
+    ap.add_argument("--backward-only", action="store_true",
+                    help="only the config-1 backward measurement (profiling runs)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic.json from two rocprofv3 --pmc runs of --profile-pass")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary[0], args.pmc_summary[1],
+                    os.path.join(ROOT, "profiles", "traffic.json"))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the GDN operator shards by "
               "heads with no communication, so --gpus N>1 is not run here.", file=sys.stderr)
@@ -490,6 +559,10 @@ def main():
     dev = torch.device("cuda:0")
     if args.profile_pass:
         profile_pass(dev)
+        return
+    if args.backward_only:
+        print(json.dumps(_backward_record(bench_backward(dev, args.steps, args.warmup), True)),
+              flush=True)
         return
 
     pre = bench_prefill(dev, args.steps, args.warmup)
