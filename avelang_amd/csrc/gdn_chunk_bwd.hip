@@ -175,16 +175,9 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
   auto step = [&](const RevIn<K>& cur, RevIn<K>& nxt, int ci, int cn) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
-    // dS' of this chunk for the gradient kernel
-    {
-      uint16_t* dst = ws.dse + ((size_t)ci * Hv + h) * K * V + 16 * vt + r16;
+    f32x4 Dsave[RT];   // dS' of this chunk, stored after the step's last prefetch
 #pragma unroll
-      for (int tt = 0; tt < RT; ++tt) {
-        const u16x4 d4 = f2bf4(Dr[tt]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[(size_t)(w * 16 * RT + 16 * tt + 4 * grp + r) * V] = d4[r];
-      }
-    }
+    for (int tt = 0; tt < RT; ++tt) Dsave[tt] = Dr[tt];
     rev_load_a<K>(nxt, ctx, cn);
     const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.G), L - 1));
     const float egx = __expf(cur.G), decx = __expf(GL - cur.G);
@@ -215,6 +208,7 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
       xc = mfma16(cur.kf[b], sl0, xc);
       xd = mfma16(cur.kf[b + 1], sl1, xd);
     }
+    u16x4 ddsave;
     // P^T dO (bf16 operands, exact products)
     const f32x4 pd = mfma16(cur.pf[1], cur.dof[1], mfma16(cur.pf[0], cur.dof[0], zero4()));
     {
@@ -224,13 +218,7 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
       split_bf4(y, yh, yl);
       *reinterpret_cast<u16x4*>(&YsT[0][r16][16 * w + 4 * grp]) = yh;
       *reinterpret_cast<u16x4*>(&YsT[1][r16][16 * w + 4 * grp]) = yl;
-      // dd rows 16w + 4grp + r (rows >= L dropped by the buffer range)
-      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
-          ws.dd + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        __builtin_amdgcn_raw_buffer_store_b16(
-            yh[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
+      ddsave = yh;
     }
     __syncthreads();
     rev_load_b<K>(nxt, ctx, cn);
@@ -283,6 +271,23 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
     }
     __syncthreads();
     rev_load_c<K>(nxt, ctx, cn);
+    // stores after the step's last prefetch: vector memory operations retire
+    // in issue order, so a store ahead of a prefetch delays that prefetch's wait
+    {
+      uint16_t* dst = ws.dse + ((size_t)ci * Hv + h) * K * V + 16 * vt + r16;
+#pragma unroll
+      for (int tt = 0; tt < RT; ++tt) {
+        const u16x4 d4 = f2bf4(Dsave[tt]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(size_t)(w * 16 * RT + 16 * tt + 4 * grp + r) * V] = d4[r];
+      }
+      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+          ws.dd + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_raw_buffer_store_b16(
+            ddsave[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
+    }
 
     // dS = e^G_L dS' + K^T (-e^G Z) + Q^T (c' e^G dO)
     {
