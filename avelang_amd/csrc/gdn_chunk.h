@@ -21,7 +21,7 @@ struct ChunkWs {
   float* tmat;      // [NC][Hv][64][64] T = (I + A)^-1 (fp32, row-major, upper part 0)
   u16x8* ttfrag;    // [NC][Hv][4][2][2][64] A-operand fragments of Tb^T (hi, lo)
   u16x8* ptfrag;    // [NC][Hv][4][2][64]    A-operand fragments of P^T
-  uint16_t* hs;     // [NC][Hv][K][V] bf16: state at the start of every chunk
+  uint16_t* hs;     // [NC][Hv][V][K] bf16: state at the start of every chunk, transposed
   uint16_t* dl;     // [B*T][Hv][V]   bf16: d = vnew, the per-token delta
 };
 

@@ -550,14 +550,13 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   auto step = [&](const ChainIn<K>& cur, ChainIn<K>& nxt, int ci, int cn) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
+    // SAVE: this thread's 16 bytes of the published bf16 state (SsT[0] =
+    // S^T of this V tile), read before the state is republished and stored
+    // after the step's last prefetch: one coalesced 16-byte store per thread
+    u16x8 hsv = {0, 0, 0, 0, 0, 0, 0, 0};
     if constexpr (SAVE) {
-      uint16_t* hd = ws.hs + ((size_t)ci * Hv + h) * K * V + 16 * vt + r16;
-#pragma unroll
-      for (int tt = 0; tt < RT; ++tt) {
-        const u16x4 s4 = f2bf4(Sr[tt]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) hd[(size_t)(w * 16 * RT + 16 * tt + 4 * grp + r) * V] = s4[r];
-      }
+      if (tid < 16 * K / 8)
+        hsv = *reinterpret_cast<const u16x8*>(&SsT[0][tid / (K / 8)][8 * (tid % (K / 8))]);
     }
     chain_load_a<K>(nxt, ctx, cn);
     // gate factors of this wave's rows 16w + 4grp + r: e^G, e^(G_last - G),
@@ -637,6 +636,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
 
     // vnew = Tb Y (three hi/lo terms, independent accumulators)
     f32x4 vn;
+    u16x4 vbs;   // bf16 vnew (the saved delta)
     {
       f32x4 va = zero4(), vb = zero4(), vc = zero4();
 #pragma unroll
@@ -655,20 +655,26 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       const u16x4 vb = f2bf4(vn);
       *reinterpret_cast<u16x4*>(&UsT[0][r16][16 * w + 4 * grp]) = uh;
       *reinterpret_cast<u16x4*>(&UsT[1][r16][16 * w + 4 * grp]) = ul;
-      if constexpr (SAVE) {
-        // delta rows 16w + 4grp + r of this chunk (rows >= L dropped by the
-        // buffer range)
-        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
-            ws.dl + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          __builtin_amdgcn_raw_buffer_store_b16(
-              vb[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
-      }
+      vbs = vb;
       if constexpr (OUT) *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
     }
     __syncthreads();
     chain_load_c<K>(nxt, ctx, cn);
+    // saves for the backward, after the step's last prefetch (vector memory
+    // operations retire in issue order: a store ahead of a prefetch would
+    // delay that prefetch's wait): the chunk's start state, transposed
+    // (hs[chunk][head] = S^T, [V][K]), and the chunk's deltas
+    if constexpr (SAVE) {
+      if (tid < 16 * K / 8)
+        *reinterpret_cast<u16x8*>(ws.hs + (((size_t)ci * Hv + h) * V + 16 * vt + tid / (K / 8)) * K +
+                                  8 * (tid % (K / 8))) = hsv;
+      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+          ws.dl + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_raw_buffer_store_b16(
+            vbs[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
+    }
 
     // S = e^G_L S + K^T U   (U hi + lo)
     {

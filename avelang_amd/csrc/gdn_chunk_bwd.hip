@@ -30,7 +30,7 @@ namespace gdn {
 
 struct BwdWs {
   ChunkWs f;              // forward workspace (gate, fragments, T, hs, dl, ...)
-  uint16_t* dse;          // [NC][Hv][K][V] bf16: dL/d(end state) of every chunk
+  uint16_t* dse;          // [NC][Hv][V][K] bf16: dL/d(end state) of every chunk, transposed
   uint16_t* dd;           // [B*T][Hv][V]   bf16: dL/dd
 };
 
@@ -175,9 +175,11 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
   auto step = [&](const RevIn<K>& cur, RevIn<K>& nxt, int ci, int cn) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
-    f32x4 Dsave[RT];   // dS' of this chunk, stored after the step's last prefetch
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) Dsave[tt] = Dr[tt];
+    // this thread's 16 bytes of the published bf16 dS' (DsT[0] = dS'^T of
+    // this V tile), stored after the step's last prefetch
+    u16x8 dsv = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (tid < 16 * K / 8)
+      dsv = *reinterpret_cast<const u16x8*>(&DsT[0][tid / (K / 8)][8 * (tid % (K / 8))]);
     rev_load_a<K>(nxt, ctx, cn);
     const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.G), L - 1));
     const float egx = __expf(cur.G), decx = __expf(GL - cur.G);
@@ -274,13 +276,9 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
     // stores after the step's last prefetch: vector memory operations retire
     // in issue order, so a store ahead of a prefetch delays that prefetch's wait
     {
-      uint16_t* dst = ws.dse + ((size_t)ci * Hv + h) * K * V + 16 * vt + r16;
-#pragma unroll
-      for (int tt = 0; tt < RT; ++tt) {
-        const u16x4 d4 = f2bf4(Dsave[tt]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[(size_t)(w * 16 * RT + 16 * tt + 4 * grp + r) * V] = d4[r];
-      }
+      if (tid < 16 * K / 8)
+        *reinterpret_cast<u16x8*>(ws.dse + (((size_t)ci * Hv + h) * V + 16 * vt + tid / (K / 8)) * K +
+                                  8 * (tid % (K / 8))) = dsv;
       const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
           ws.dd + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
 #pragma unroll
@@ -390,7 +388,14 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   static_assert(NPOS <= NTH, "one staged position per thread");
   __shared__ __attribute__((aligned(16))) uint16_t Ks[64][LK];
   __shared__ __attribute__((aligned(16))) uint16_t Qs[64][LK];
-  __shared__ __attribute__((aligned(16))) uint16_t Stg[2][2][32][LV];   // [buf][matrix][row]
+  // stage of the streamed slices: state slices [buf][matrix][V rows][32 + 8
+  // columns] (rows of S^T / dS'^T), token slices [buf][matrix][32 rows][LV]
+  constexpr int LS = 40;
+  constexpr int kStgBytes = (2 * 2 * V * LS * 2 > 2 * 2 * 32 * LV * 2) ? 2 * 2 * V * LS * 2
+                                                                        : 2 * 2 * 32 * LV * 2;
+  __shared__ __attribute__((aligned(16))) unsigned char StgRaw[kStgBytes];
+  uint16_t (*StgS)[2][V][LS] = reinterpret_cast<uint16_t (*)[2][V][LS]>(StgRaw);
+  uint16_t (*Stg)[2][32][LV] = reinterpret_cast<uint16_t (*)[2][32][LV]>(StgRaw);
   __shared__ __attribute__((aligned(16))) float T32[64][LT];
   __shared__ __attribute__((aligned(16))) float X32[64][LT];
   __shared__ __attribute__((aligned(16))) uint16_t Tb16[64][LC];
@@ -489,8 +494,11 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const int row0 = 16 * rt + 4 * grp;
     // staged position of this thread in a slice (both matrices)
     const bool stager = tid < NPOS;
+    // token slice position: row sp_r, columns sp_c8..+7; state slice
+    // position: S^T row ss_v, state columns ss_k..+7 of the slice
     const int sp_r = (tid % NPOS) / (V / 8), sp_c8 = 8 * (tid % (V / 8));
-    const int sp_vs = (sp_r * V + sp_c8) * 2;            // byte offset in a state slice
+    const int ss_v = (tid % NPOS) / 4, ss_k = 8 * (tid % 4);
+    const int sp_vs = (ss_v * K + ss_k) * 2;             // byte offset in a state slice
     const int sp_vt = (sp_r * Hv * V + sp_c8) * 2;       // byte offset in a token slice
     const int h = hq * Gn + gi;
     const size_t ch = (size_t)ci * Hv + h;
@@ -509,13 +517,14 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
 
-    // slice sl: rows 32 sl.. of S (matrix 0) and dS' (matrix 1) for sl < NSS,
+    // slice sl: state columns 32 sl..32 sl + 31 of every row of S^T (matrix
+    // 0) and dS'^T (matrix 1) for sl < NSS (both stored transposed, [V][K]),
     // token rows 32 (sl - NSS).. of d (0) and V (1) after
     float sde = 0.f;   // partial <S, dS'> of the positions this thread stages
     auto load_slice = [&](int sl, u16x8 (&buf)[2]) {
       if (!stager) return;
       if (sl < NSS) {
-        const int so = 32 * sl * V * 2;
+        const int so = 32 * sl * 2;
         buf[0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rS, sp_vs, so, 0));
         buf[1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rE, sp_vs, so, 0));
       } else {
@@ -526,8 +535,13 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     };
     auto store_slice = [&](int sl, const u16x8 (&buf)[2]) {
       if (!stager) return;
-      *reinterpret_cast<u16x8*>(&Stg[sl & 1][0][sp_r][sp_c8]) = buf[0];
-      *reinterpret_cast<u16x8*>(&Stg[sl & 1][1][sp_r][sp_c8]) = buf[1];
+      if (sl < NSS) {
+        *reinterpret_cast<u16x8*>(&StgS[sl & 1][0][ss_v][ss_k]) = buf[0];
+        *reinterpret_cast<u16x8*>(&StgS[sl & 1][1][ss_v][ss_k]) = buf[1];
+      } else {
+        *reinterpret_cast<u16x8*>(&Stg[sl & 1][0][sp_r][sp_c8]) = buf[0];
+        *reinterpret_cast<u16x8*>(&Stg[sl & 1][1][sp_r][sp_c8]) = buf[1];
+      }
       if (sl < NSS) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) sde += bf2f(buf[0][j]) * bf2f(buf[1][j]);
@@ -609,8 +623,14 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       f32x4 x0 = zero4(), x1 = zero4(), x2 = zero4();
 #pragma unroll
       for (int b = 0; b < VB; ++b) {
-        const u16x8 b0 = *reinterpret_cast<const u16x8*>(&Stg[bufi][0][16 * hf + r16][32 * b + 8 * grp]);
-        const u16x8 b1 = *reinterpret_cast<const u16x8*>(&Stg[bufi][1][16 * hf + r16][32 * b + 8 * grp]);
+        // B[k = v][n = state column 16 hf + r16]: columns of the staged S^T /
+        // dS'^T rows; B[k = v][n = token row 16 hf + r16]: staged d / V rows
+        const u16x8 b0 = sl < NSS
+            ? lds_colfrag(&StgS[bufi][0][0][0], LS, 32 * b, 16 * hf, lane)
+            : *reinterpret_cast<const u16x8*>(&Stg[bufi][0][16 * hf + r16][32 * b + 8 * grp]);
+        const u16x8 b1 = sl < NSS
+            ? lds_colfrag(&StgS[bufi][1][0][0], LS, 32 * b, 16 * hf, lane)
+            : *reinterpret_cast<const u16x8*>(&Stg[bufi][1][16 * hf + r16][32 * b + 8 * grp]);
         if (sl < NSS) {
           x0 = mfma16(aO[b], b0, x0);    // dO S^T
           x1 = mfma16(aD[b], b0, x1);    // dd S^T
