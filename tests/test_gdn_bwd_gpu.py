@@ -238,3 +238,15 @@ def test_autograd_without_saved_forward(rocm_device, monkeypatch):
         grads.append([x.grad for x in leaves])
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+def test_bwd_varlen_many_sequences(rocm_device):
+    """Config 3's structure (packed sequences of lengths U[128, 4096], seeded) at 8 sequences
+    and 2 qk-heads -> 4 v-heads, so the fp64 oracle stays fast."""
+    cu = W.varlen_cu_seqlens(8, 128, 4096, seed=3)
+    _case(rocm_device, 1, int(cu[-1]), 2, 4, 128, 128, seed=50, cu=cu, what="varlen 8 seqs")
+
+
+def test_bwd_long_context(rocm_device):
+    """Config 4's slow decay over a 16384-token sequence (256 chunks), 1 qk-head -> 2 v-heads."""
+    _case(rocm_device, 1, 16384, 1, 2, 128, 128, seed=51, decay=0.01, what="T16384 decay .01")
