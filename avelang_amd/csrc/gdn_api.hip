@@ -31,7 +31,7 @@ int check_launch(const char* what) {
   return GDN_OK;
 }
 
-static bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
   auto pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
   return pa < pb + nb && pb < pa + na;
 }

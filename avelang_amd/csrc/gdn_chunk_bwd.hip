@@ -1004,6 +1004,24 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   const long long tokens = (long long)B * T;
   if (tokens > 0 && (!dq || !dk || !dv || !dg || !dbeta))
     return gdn_host::fail(GDN_ERR_NULL, "gdn_chunk_bwd: dq, dk, dv, dg and dbeta must be non-NULL");
+  {
+    // the gradients are written while the inputs are still being read: no
+    // output may share memory with an input or with another output
+    const size_t nqk = (size_t)tokens * Hqk * K * 2, nv = (size_t)tokens * Hv * V * 2;
+    const size_t ng = (size_t)tokens * Hv * 4, ns = (size_t)N * Hv * K * V * 4;
+    const void* in[] = {q, k, v, g, beta, h0, dO, dht};
+    const size_t nin[] = {nqk, nqk, nv, ng, ng, h0 ? ns : 0, nv, dht ? ns : 0};
+    const void* out[] = {dq, dk, dv, dg, dbeta, dh0};
+    const size_t nout[] = {nqk, nqk, nv, ng, ng, dh0 ? ns : 0};
+    for (int i = 0; i < 6; ++i) {
+      for (int j = 0; j < 8; ++j)
+        if (out[i] && in[j] && gdn_host::overlaps(out[i], nout[i], in[j], nin[j]))
+          return gdn_host::fail(GDN_ERR_ALIAS, "gdn_chunk_bwd: a gradient buffer overlaps an input");
+      for (int j = i + 1; j < 6; ++j)
+        if (out[i] && out[j] && gdn_host::overlaps(out[i], nout[i], out[j], nout[j]))
+          return gdn_host::fail(GDN_ERR_ALIAS, "gdn_chunk_bwd: two gradient buffers overlap");
+    }
+  }
   if (N == 0 || (tokens == 0 && !dh0)) return GDN_OK;
   const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
                                      use_qk_l2norm != 0, true);

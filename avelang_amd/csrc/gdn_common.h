@@ -80,4 +80,6 @@ namespace gdn_host {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+// [a, a + na) and [b, b + nb) share a byte (callers skip NULL pointers).
+bool overlaps(const void* a, size_t na, const void* b, size_t nb);
 }  // namespace gdn_host

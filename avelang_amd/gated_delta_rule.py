@@ -21,6 +21,7 @@ from __future__ import annotations
 from typing import Optional, Tuple
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from . import _native
 
@@ -262,6 +263,7 @@ class _ChunkGatedDeltaRule(torch.autograd.Function):
         return o
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, do, dht=None):
         q, k, v, g, beta, h0, cu = ctx.saved_tensors
         if dht is not None and not ctx.has_ht:

@@ -83,6 +83,48 @@ def test_argument_errors(lib, fn, kw, code, msg):
     assert msg in _native.last_error()
 
 
+def _bwd(lib, ws=None, wsb=0, **kw):
+    M = 1 << 20
+    p = dict(q=1 * M, k=2 * M, v=3 * M, g=4 * M, beta=5 * M, h0=None, do=6 * M, dht=None,
+             dq=7 * M, dk=8 * M, dv=9 * M, dg=10 * M, db=11 * M, dh0=None, cu=None,
+             B=1, T=4, Hqk=2, Hv=4, K=128, V=128, N=1, scale=0.1, l2=0, saved=0, stream=None)
+    p.update(kw)
+    return lib.gdn_chunk_bwd(p["q"], p["k"], p["v"], p["g"], p["beta"], p["h0"], p["do"],
+                             p["dht"], p["dq"], p["dk"], p["dv"], p["dg"], p["db"], p["dh0"],
+                             p["cu"], p["B"], p["T"], p["Hqk"], p["Hv"], p["K"], p["V"], p["N"],
+                             p["scale"], p["l2"], p["saved"], ws, wsb, p["stream"])
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(Hv=3), -2, "multiple of Hqk"),
+    (dict(dq=None), -1, "must be non-NULL"),
+    (dict(dbeta=None, db=None), -1, "must be non-NULL"),
+    (dict(dq=(1 << 20) + 64), -5, "overlaps an input"),
+    (dict(dv=(6 << 20) + 128), -5, "overlaps an input"),
+    (dict(dk=(7 << 20) + 32), -5, "two gradient buffers overlap"),
+    (dict(do=2 << 20), -5, "must not overlap"),
+])
+def test_bwd_argument_errors(lib, kw, code, msg):
+    from avelang_amd import _native
+    kw.pop("dbeta", None)
+    assert _bwd(lib, **kw) == code
+    assert msg in _native.last_error()
+
+
+def test_bwd_workspace_checked_before_launch(lib):
+    from avelang_amd import _native
+    need = lib.gdn_chunk_bwd_workspace_bytes(1, 4, 2, 4, 128, 128, 1, 0, 0)
+    fwd = lib.gdn_chunk_workspace_bytes(1, 4, 2, 4, 128, 128, 1, 0, 0)
+    assert need > fwd > 0
+    assert _bwd(lib) == -4
+    assert "workspace needs" in _native.last_error()
+    assert _bwd(lib, ws=64 << 20, wsb=need - 1) == -4
+    # the training forward takes the backward's (larger) workspace
+    rc = lib.gdn_chunk_fwd_save(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, None, None, 6 << 20,
+                                None, 1, 4, 2, 4, 128, 128, 1, 0.1, 0, 64 << 20, fwd, None)
+    assert rc == -4 and "gdn_chunk_fwd_save" in _native.last_error()
+
+
 def test_chunk_workspace_checked_before_launch(lib):
     from avelang_amd import _native
     need = lib.gdn_chunk_workspace_bytes(1, 4, 2, 4, 128, 128, 1, 0, 0)
