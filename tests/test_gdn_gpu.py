@@ -101,6 +101,30 @@ def test_decode_steps_equal_multitoken(rocm_device):
     _check(torch.cat(outs, 1), o_ref, state, s_ref, "stepwise")
 
 
+def test_decode_1000_steps_in_place(rocm_device):
+    """Config 2's 1000 consecutive in-place decode steps (16 sequences, its head shape):
+    the state after step-by-step decoding matches the oracle run over the whole 1000-token
+    sequences, so no drift accumulates over the steps."""
+    from avelang_amd import fused_recurrent_gated_delta_rule
+    wl = W.make(16, 1000, 16, 32, 128, 128, seed=12, h0_scale=0.01)
+    o_ref, s_ref = _oracle("recurrent", wl)
+    t = wl.torch(rocm_device)
+    state = t["initial_state"].clone()
+    ptr = state.data_ptr()
+    outs = []
+    for i in range(1000):
+        sl = lambda x: x[:, i:i + 1].contiguous()  # noqa: E731
+        o, st = fused_recurrent_gated_delta_rule(sl(t["q"]), sl(t["k"]), sl(t["v"]), sl(t["g"]),
+                                                 sl(t["beta"]), initial_state=state,
+                                                 output_final_state=True,
+                                                 inplace_final_state=True)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert st.data_ptr() == ptr
+    fro = _check(torch.cat(outs, 1), o_ref, state, s_ref, "1000 decode steps")
+    print(f"1000 decode steps: state rel fro {fro:.2e}", flush=True)
+
+
 @pytest.mark.parametrize("K,V", [(64, 64), (128, 64), (64, 128)])
 def test_decode_head_sizes(rocm_device, K, V):
     wl = W.make(4, 5, 2, 4, K, V, seed=K + V, h0_scale=0.01)
