@@ -372,10 +372,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 }
 
 // --------------------------------------------------------- chain (K2) ----
-// Operands of one chunk step for wave w (chunk rows 16w..16w+15), fetched one
-// step ahead in parts so the vector-memory queue never stalls a wave for
-// long: A (K rows) before the K S products, B (Tb, P fragments) and Q rows
-// after the first barrier, C (V column slice, G) after the second.
+// Operands of one chunk step for wave w (chunk rows 16w..16w+15), fetched
+// ahead in parts so the vector-memory queue never stalls a wave for long:
+// A (K rows) before the K S products, B (Tb, P fragments) and Q rows after
+// the first barrier, all one step ahead; C (V column slice, G) after the
+// second barrier, two steps ahead.
 template <int K>
 struct ChainIn {
   static constexpr int KB = K / 32;
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
   // One chunk step on `cur` (chunk ci) while `nxt` is filled for chunk cn.
   // Every accumulation is split over independent accumulators so no MFMA
   // chain is more than two deep (a dependent 16x16x32 MFMA costs ~34 cycles).
-  auto step = [&](const ChainIn<K>& cur, ChainIn<K>& nxt, int ci, int cn) {
+  auto step = [&](ChainIn<K>& cur, ChainIn<K>& nxt, int ci, int cn, int cn2) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
     // SAVE: this thread's 16 bytes of the published bf16 state (SsT[0] =
@@ -659,7 +660,10 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
       if constexpr (OUT) *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
     }
     __syncthreads();
-    chain_load_c<K>(nxt, ctx, cn);
+    // V and G two chunks ahead, into this step's own buffer (its V and G
+    // were last read in the first phase): they are the first operands a
+    // step waits for, and one step of lead left that wait exposed
+    chain_load_c<K>(cur, ctx, cn2);
     // saves for the backward, after the step's last prefetch (vector memory
     // operations retire in issue order: a store ahead of a prefetch would
     // delay that prefetch's wait): the chunk's start state, transposed
@@ -729,12 +733,23 @@ __global__ __launch_bounds__(256) void chunk_chain_kernel(
     chain_load_b<K>(bufA, ctx, c_begin);
     chain_load_q<K>(bufA, ctx, c_begin);
     chain_load_c<K>(bufA, ctx, c_begin);
+    chain_load_c<K>(bufB, ctx, min(c_begin + 1, c_end - 1));
   }
-  for (int ci = c_begin; ci < c_end; ci += 2) {
-    step(bufA, bufB, ci, min(ci + 1, c_end - 1));
-    if (ci + 1 >= c_end) break;
-    step(bufB, bufA, ci + 1, min(ci + 2, c_end - 1));
+  // Nothing outstanding on entry: the wait counts at the loop head merge the
+  // entry path with the back edge, and the prologue's loads (issued in
+  // another order than the loop's) made that merge wait for nearly every
+  // prefetch at each step start.  The first step needs these loads anyway.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  // Pairs of steps, then an odd last chunk outside the loop: an exit between
+  // the two steps of a pair would be a path back to the loop head after one
+  // step, and the wait counts there would have to cover it (a wait for
+  // nearly every outstanding prefetch at each pair's start).
+  int ci = c_begin;
+  for (; ci + 1 < c_end; ci += 2) {
+    step(bufA, bufB, ci, ci + 1, min(ci + 2, c_end - 1));
+    step(bufB, bufA, ci + 1, min(ci + 2, c_end - 1), min(ci + 3, c_end - 1));
   }
+  if (ci < c_end) step(bufA, bufB, ci, ci, ci);
 
   if (ht) {
 #pragma unroll

@@ -21,6 +21,9 @@ constexpr int kChunk = 64;  // tokens per chunk of the prefill path
 // return 0 and out-of-range stores are dropped.
 constexpr int kBufferFlags = 0x00020000;
 constexpr int kWave = 64;   // CDNA wavefront width
+// s_waitcnt immediate (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8) that waits for every vector-memory load and nothing else.
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // bf16 <-> fp32 on raw 16-bit patterns.
 __device__ __forceinline__ float bf2f(uint16_t x) {
