@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
   publish();
   __syncthreads();
 
-  auto step = [&](const RevIn<K>& cur, RevIn<K>& nxt, int ci, int cn) {
+  auto step = [&](RevIn<K>& cur, RevIn<K>& nxt, int ci, int cn, int cn2) {
     const int t0 = s + (ci - c_begin) * kChunk;
     const int L = min(kChunk, e - t0);
     // this thread's 16 bytes of the published bf16 dS' (DsT[0] = dS'^T of
@@ -272,7 +272,9 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
       ol[kb] = u16x8{l0v[0], l0v[1], l0v[2], l0v[3], l1v[0], l1v[1], l1v[2], l1v[3]};
     }
     __syncthreads();
-    rev_load_c<K>(nxt, ctx, cn);
+    // dO and G two chunks ahead, into this step's own buffer (last read
+    // before the second barrier): the first operands a step waits for
+    rev_load_c<K>(cur, ctx, cn2);
     // stores after the step's last prefetch: vector memory operations retire
     // in issue order, so a store ahead of a prefetch delays that prefetch's wait
     {
@@ -317,12 +319,18 @@ __global__ __launch_bounds__(256) void chunk_rev_kernel(
     rev_load_a<K>(bufA, ctx, c_end - 1);
     rev_load_b<K>(bufA, ctx, c_end - 1);
     rev_load_c<K>(bufA, ctx, c_end - 1);
+    rev_load_c<K>(bufB, ctx, max(c_end - 2, c_begin));
   }
-  for (int ci = c_end - 1; ci >= c_begin; ci -= 2) {
-    step(bufA, bufB, ci, max(ci - 1, c_begin));
-    if (ci - 1 < c_begin) break;
-    step(bufB, bufA, ci - 1, max(ci - 2, c_begin));
+  // Nothing outstanding on entry, and pairs of steps with an odd last chunk
+  // outside the loop, so the wait counts at the loop head cover only the
+  // prefetch the next step needs (see the forward chain).
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  int ci = c_end - 1;
+  for (; ci - 1 >= c_begin; ci -= 2) {
+    step(bufA, bufB, ci, ci - 1, max(ci - 2, c_begin));
+    step(bufB, bufA, ci - 1, max(ci - 2, c_begin), max(ci - 3, c_begin));
   }
+  if (ci >= c_begin) step(bufA, bufB, ci, ci, ci);
 
   if (dh0) {
 #pragma unroll
