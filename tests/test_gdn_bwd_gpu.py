@@ -173,6 +173,18 @@ def test_autograd_matches_bwd(rocm_device):
         assert torch.equal(a.float(), got[key].float()), f"autograd {n} differs from the bwd call"
 
 
+def test_bwd_linear_in_output_gradients(rocm_device):
+    """No oracle: the gradients are linear in (dO, dht), and every step of the backward commutes
+    with doubling (bf16 hi/lo splits, MFMA products and fp32 sums of doubled operands), so
+    doubling dO and dht doubles every gradient bit for bit (config 1's heads, T = 1000)."""
+    wl = W.make(1, 1000, 16, 32, 128, 128, seed=31, h0_scale=0.01)
+    do, dht = _grad_inputs(wl, 31)
+    a = _gpu_bwd(wl, do, dht, rocm_device)
+    b = _gpu_bwd(wl, 2 * do, 2 * dht, rocm_device)
+    for name in a:
+        assert torch.equal(b[name], 2 * a[name]), name
+
+
 def test_bwd_deterministic(rocm_device):
     wl = W.make(1, 300, 2, 4, 128, 128, seed=31)
     do, dht = _grad_inputs(wl, 31)

@@ -294,6 +294,73 @@ def test_prefill_deterministic(rocm_device):
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
 
 
+def test_prefill_homogeneous_cfg1(rocm_device):
+    """Config 1 in full, no oracle: the recurrence is jointly linear in (h0, v), and every step
+    of the kernels commutes with doubling (bf16 hi/lo splits, MFMA products and fp32 sums of
+    doubled operands are the doubled results), so doubling h0 and v doubles o and the final state
+    bit for bit."""
+    from avelang_amd import chunk_gated_delta_rule
+    t = W.config("cfg1_prefill_qwen3next", seed=21).torch(rocm_device)
+    o1, s1 = chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
+                                    initial_state=t["initial_state"], output_final_state=True)
+    o2, s2 = chunk_gated_delta_rule(t["q"], t["k"], 2 * t["v"], t["g"], t["beta"],
+                                    initial_state=2 * t["initial_state"], output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, 2 * o1)
+    assert torch.equal(s2, 2 * s1)
+
+
+def test_prefill_beta_zero_pure_decay_cfg1(rocm_device):
+    """Config 1's shape with beta = 0, against the closed form instead of the oracle: the delta
+    rule is off, so S_t = e^{G_t} S_0 and o_t = scale e^{G_t} S_0^T q_t with G_t the cumulative
+    log-decay (slow decay so that e^{G_T} stays well inside fp32)."""
+    wl = W.config("cfg1_prefill_qwen3next", seed=22, decay=0.001)
+    wl.beta[:] = 0
+    o, s = _run_chunk(wl, rocm_device)
+    a = wl.numpy()
+    G = np.cumsum(a["g"][0].astype(np.float64), axis=0)                  # [T, Hv]
+    h0 = a["initial_state"][0].astype(np.float64)                        # [Hv, K, V]
+    qv = np.repeat(a["q"][0].astype(np.float64), 2, axis=1)              # [T, Hv, K]
+    qs = np.matmul(qv.transpose(1, 0, 2), h0).transpose(1, 0, 2)        # [T, Hv, V]
+    o_ref = (128 ** -0.5) * np.exp(G)[..., None] * qs
+    s_ref = np.exp(G[-1])[:, None, None] * h0
+    o_np = _np(o)[0]
+    o_fro = np.linalg.norm(o_np - o_ref) / np.linalg.norm(o_ref)
+    s_fro = np.linalg.norm(_np(s)[0] - s_ref) / np.linalg.norm(s_ref)
+    print(f"beta = 0: o rel fro {o_fro:.2e}, state rel fro {s_fro:.2e}", flush=True)
+    assert np.allclose(o_np, o_ref, atol=O_TOL, rtol=O_TOL)
+    assert o_fro <= 1e-2, o_fro     # bf16 output and the bf16 S in Q S: ~2^-9
+    assert s_fro <= S_FRO, s_fro
+
+
+def test_decode_unit_key_retrieval_cfg2(rocm_device):
+    """Config 2's batch and heads, g = 0, beta = 1, in-kernel l2norm: after one step the state
+    returns the written value for the normalised key, S_1^T k = (1 - |k|^2) S_0^T k + |k|^2 v,
+    which is v up to the 1e-6 of the l2norm epsilon."""
+    from avelang_amd import fused_recurrent_gated_delta_rule
+    wl = W.config("cfg2_decode_b256", seed=23)
+    wl.g[:] = 0
+    wl.beta[:] = 1
+    t = wl.torch(rocm_device)
+    state = t["initial_state"].clone()
+    _, st = fused_recurrent_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
+                                             initial_state=state, output_final_state=True,
+                                             inplace_final_state=True,
+                                             use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    k = t["k"].double()[:, 0]                                            # [N, Hqk, K]
+    kn = (k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)).repeat_interleave(2, dim=1)
+    s0 = t["initial_state"].double()
+    v = t["v"].double()[:, 0]
+    nk2 = (kn * kn).sum(-1, keepdim=True)
+    want = (1 - nk2) * torch.einsum("nhkv,nhk->nhv", s0, kn) + nk2 * v
+    got = torch.einsum("nhkv,nhk->nhv", st.double(), kn)
+    err = (got - want).abs().max().item()
+    print(f"unit-key retrieval: max |S^T k - v| deviation {err:.2e}", flush=True)
+    assert err <= 1e-4, err
+    assert (want - v).abs().max().item() <= 1e-5
+
+
 def test_prefill_l2norm_in_kernel(rocm_device):
     """In-kernel l2norm rounds the normalised q, k to bf16 (FLA's l2norm pass)."""
     wl = W.make(1, 200, 4, 8, 128, 128, seed=88, h0_scale=0.01, l2norm=False)
