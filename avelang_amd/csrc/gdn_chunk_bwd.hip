@@ -24,6 +24,8 @@
 //   chunk_grad_kernel   one workgroup per (chunk, qk-head), fully parallel:
 //                       the local gradients of the group's v-heads, dq / dk
 //                       summed over the group in registers
+#include <type_traits>
+
 #include "gdn_chunk.h"
 
 namespace gdn {
@@ -486,7 +488,85 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   }
 
   const int vbytes = L * Hv * V * 2;
-  for (int gi = 0; gi < Gn; ++gi) {
+  // Operands of a v-head's staging phase (slices 0..2 of S / dS' or d / V,
+  // T, the dd rows, G and beta, the A fragments of dO / dd / d), requested
+  // into registers: for the first v-head here, for each later one before the
+  // previous v-head's dK / dQ products, so their latency overlaps that
+  // v-head's last phases instead of opening the next one.
+  constexpr int NT = 64 * 16 / NTH, ND = 64 * V / 8 / NTH;
+  u16x8 pre[3][2];
+  f32x4 tv[NT];
+  u16x8 dv8[ND];
+  u16x8 aO[VB], aD[VB], aL[VB];
+  float gsv = 0.f, bsv = 0.f;
+  auto issue_stage = [&](int gi_t) {
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid % 64;
+    const int rt = __builtin_amdgcn_readfirstlane(tid / 64) & 3;
+    const int r16 = lane % 16, grp = lane / 16;
+    const int rowA = 16 * rt + r16;
+    const int sp_r = (tid % NPOS) / (V / 8), sp_c8 = 8 * (tid % (V / 8));
+    const int ss_v = (tid % NPOS) / 4, ss_k = 8 * (tid % 4);
+    const int sp_vs = (ss_v * K + ss_k) * 2;
+    const int sp_vt = (sp_r * Hv * V + sp_c8) * 2;
+    const int h = hq * Gn + gi_t;
+    const size_t ch = (size_t)ci * Hv + h;
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
+        ws.f.hs + ch * K * V, 0, K * V * 2, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rE = __builtin_amdgcn_make_buffer_rsrc(
+        ws.dse + ch * K * V, 0, K * V * 2, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rT = __builtin_amdgcn_make_buffer_rsrc(
+        ws.f.tmat + ch * 64 * 64, 0, 64 * 64 * 4, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rdd = __builtin_amdgcn_make_buffer_rsrc(
+        ws.dd + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
+        ws.f.dl + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
+    if (tid < NPOS) {
+#pragma unroll
+      for (int sl = 0; sl < 3 && sl < NSL; ++sl) {
+        if (sl < NSS) {
+          const int so = 32 * sl * 2;
+          pre[sl][0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rS, sp_vs, so, 0));
+          pre[sl][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rE, sp_vs, so, 0));
+        } else {
+          const int so = 32 * (sl - NSS) * Hv * V * 2;
+          pre[sl][0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_vt, so, 0));
+          pre[sl][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, sp_vt, so, 0));
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+      tv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rT, 16 * tid, 16 * NTH * i, 0));
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int idx = tid + NTH * i, r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
+      dv8[i] = __builtin_bit_cast(
+          u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, (r * Hv * V + c8) * 2, 0, 0));
+    }
+    if (tid < 64) {
+      gsv = ws.f.gate[ch * 64 + tid];
+      bsv = tid < L ? beta[(size_t)(t0 + min(tid, L - 1)) * Hv + h] : 0.f;
+    }
+#pragma unroll
+    for (int b = 0; b < VB; ++b) {
+      const int off = (rowA * Hv * V + 32 * b + 8 * grp) * 2;
+      aO[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
+      aD[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, off, 0, 0));
+      aL[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
+    }
+  };
+  issue_stage(0);
+  // One v-head of the group.  Instantiated with and without the next
+  // v-head's prefetch, so that the prefetch is unconditional where it is
+  // made (a conditional one keeps the previous operands live through the
+  // whole v-head for the path that skips it, which spills).
+  auto vhead = [&](int gi, auto prefetch_next) {
     // The lane index is passed through an empty asm statement once per
     // v-head, so the many per-lane LDS / buffer addresses derived from it are
     // formed inside the loop where they are used, instead of being hoisted
@@ -556,39 +636,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
     };
 
-    // ---- issued before the first wait: slices 0..2, T, G, beta, dd rows,
-    // the A fragments
-    u16x8 pre[3][2];
-    load_slice(0, pre[0]);
-    load_slice(1, pre[1]);
-    if (NSL > 2) load_slice(2, pre[2]);
-    constexpr int NT = 64 * 16 / NTH, ND = 64 * V / 8 / NTH;
-    f32x4 tv[NT];
-    u16x8 dv8[ND];
-    {
-#pragma unroll
-      for (int i = 0; i < NT; ++i)
-        tv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rT, 16 * tid, 16 * NTH * i, 0));
-#pragma unroll
-      for (int i = 0; i < ND; ++i) {
-        const int idx = tid + NTH * i, r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
-        dv8[i] = __builtin_bit_cast(
-            u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, (r * Hv * V + c8) * 2, 0, 0));
-      }
-    }
-    float gsv = 0.f, bsv = 0.f;
-    if (tid < 64) {
-      gsv = ws.f.gate[ch * 64 + tid];
-      bsv = tid < L ? beta[(size_t)(t0 + min(tid, L - 1)) * Hv + h] : 0.f;
-    }
-    u16x8 aO[VB], aD[VB], aL[VB];
-#pragma unroll
-    for (int b = 0; b < VB; ++b) {
-      const int off = (rowA * Hv * V + 32 * b + 8 * grp) * 2;
-      aO[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
-      aD[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, off, 0, 0));
-      aL[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
-    }
+    // ---- staging: the operands issue_stage() requested for this v-head
     __builtin_amdgcn_sched_barrier(0);
     store_slice(0, pre[0]);
 #pragma unroll
@@ -804,6 +852,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       Cv[tid] = cv;
     }
 
+    if constexpr (decltype(prefetch_next)::value) issue_stage(gi + 1);
+
     // ---- dK += M K + M^T K + MP^T Q,  dQ += MP K (this wave's column tiles)
     {
       u16x8 am[2], amt[2], ap[2], apt[2];
@@ -886,7 +936,9 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       if (ir < L) dg[(size_t)(t0 + ir) * Hv + h] = x;
     }
     __syncthreads();   // LDS reuse by the next v-head
-  }
+  };
+  for (int gi = 0; gi + 1 < Gn; ++gi) vhead(gi, std::true_type{});
+  vhead(Gn - 1, std::false_type{});
 
   // ---- dq, dk: through the l2norm when the forward normalised q, k
   const __amdgpu_buffer_rsrc_t rdq = __builtin_amdgcn_make_buffer_rsrc(
