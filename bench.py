@@ -386,8 +386,11 @@ def cpu_decode(runs=3):
                 sample=f"one full config-2 decode step (256 x 32 state tiles), median of {runs}")
 
 
-def profile_pass(dev, reps=3):
+def profile_pass(dev, reps=3, what="all"):
     """Fixed, untimed launch sequence for rocprofv3 counter runs.
+
+    ``what`` = "prefill" stops after step 2 (counter passes over the prefill
+    kernels alone); "all" runs every step below.
 
     1. one device-to-device copy of exactly 256 MiB (calibrates FETCH_SIZE /
        WRITE_SIZE against known bytes: 256 MiB read, 256 MiB written);
@@ -412,6 +415,9 @@ def profile_pass(dev, reps=3):
         chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
                                initial_state=t["initial_state"], output_final_state=True)
     torch.cuda.synchronize(dev)
+    if what == "prefill":
+        print("profile pass done", flush=True)
+        return
     for _ in range(reps):
         fused_recurrent_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"],
                                          initial_state=d["initial_state"],
@@ -499,6 +505,32 @@ def pmc_summary(fetch_dir, write_dir, out_path):
     print(json.dumps({k: res[k] for k in ("prefill", "decode", "backward")}))
 
 
+def pmc_table(dirs):
+    """Per-kernel, per-dispatch averages of every counter in rocprofv3 --pmc CSV output.
+
+    Values are summed over the counter's dimensions (SEs, XCDs) within a
+    dispatch, then averaged over the dispatches of the kernel.  Printed as one
+    JSON object per kernel, keyed by counter name.
+    """
+    import csv
+    import glob
+
+    acc = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"].split("(")[0].replace("void ", "").strip()
+                disp = r.get("Dispatch_Id") or r.get("Correlation_Id")
+                key = (name, r["Counter_Name"])
+                acc.setdefault(key, {}).setdefault(disp, 0.0)
+                acc[key][disp] += float(r["Counter_Value"])
+    table = {}
+    for (name, ctr), per in acc.items():
+        table.setdefault(name, {})[ctr] = float(np.mean(list(per.values())))
+    for name in sorted(table):
+        print(json.dumps({"kernel": name, **{k: round(v, 1) for k, v in sorted(table[name].items())}}))
+
+
 def _backward_record(bwd, no_cpu):
     flops = backward_flops(bwd["T"], bwd["Hv"], bwd["K"], bwd["V"])
     tf = flops / (bwd["ms"] * 1e-3) / 1e12
@@ -536,13 +568,20 @@ def main():
                     help="skip the layer-operator measurements")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the config-1 prefill and config-2 decode lines (profiling runs)")
-    ap.add_argument("--profile-pass", action="store_true",
-                    help="run the fixed untimed launch sequence used for rocprofv3 --pmc runs")
+    ap.add_argument("--profile-pass", nargs="?", const="all", choices=("all", "prefill"),
+                    help="run the fixed untimed launch sequence used for rocprofv3 --pmc runs "
+                         "(prefill: the config-1 prefill calls only)")
+    ap.add_argument("--pmc-table", nargs="+", metavar="DIR",
+                    help="print per-kernel averages of every counter found in rocprofv3 --pmc "
+                         "output directories (one JSON object per kernel)")
     ap.add_argument("--backward-only", action="store_true",
                     help="only the config-1 backward measurement (profiling runs)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic.json from two rocprofv3 --pmc runs of --profile-pass")
     args = ap.parse_args()
+    if args.pmc_table:
+        pmc_table(args.pmc_table)
+        return
     if args.pmc_summary:
         pmc_summary(args.pmc_summary[0], args.pmc_summary[1],
                     os.path.join(ROOT, "profiles", "traffic.json"))
@@ -556,7 +595,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     if args.profile_pass:
-        profile_pass(dev)
+        profile_pass(dev, what=args.profile_pass)
         return
     if args.backward_only:
         print(json.dumps(_backward_record(bench_backward(dev, args.steps, args.warmup), True)),
