@@ -32,6 +32,7 @@ EXPORTS = (
     "gdn_causal_conv1d_update",
     "gdn_rmsnorm_gated_fwd",
     "gdn_recurrent_fwd_indexed",
+    "gdn_recurrent_fwd_spec",
 )
 
 GDN_DTYPE_F32 = 0
@@ -133,6 +134,12 @@ def lib():
         h.gdn_recurrent_fwd_indexed.restype = _i
         h.gdn_recurrent_fwd_indexed.argtypes = (
             [_vp] * 10                        # q k v g beta h0 ht o cu_seqlens state_indices
+            + [_i] * 8                        # B T Hqk Hv K V N num_slots
+            + [_f, _i, _vp])
+        h.gdn_recurrent_fwd_spec.restype = _i
+        h.gdn_recurrent_fwd_spec.argtypes = (
+            [_vp] * 9                         # q k v g beta pool o cu_seqlens state_indices
+            + [_i, _vp]                       # index_stride num_accepted_tokens
             + [_i] * 8                        # B T Hqk Hv K V N num_slots
             + [_f, _i, _vp])
         _lib = h

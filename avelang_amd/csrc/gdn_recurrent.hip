@@ -50,7 +50,8 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     const float* __restrict__ beta, const float* h0, float* ht,
     uint16_t* __restrict__ o, const int32_t* __restrict__ cu, int T,
     int total_tokens, int Hqk, int Hv, float scale, int l2norm,
-    const int32_t* __restrict__ slots, int num_slots, int ntiles) {
+    const int32_t* __restrict__ slots, int num_slots, int ntiles, int slot_stride,
+    const int32_t* __restrict__ accepted) {
   constexpr int COLG = V / 4;          // float4 column groups per row
   constexpr int ROWG = NT / COLG;      // row groups
   constexpr int RPT = K / ROWG;        // rows per lane
@@ -69,13 +70,22 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
   const int lane = tid % 64;
   const int G = gridDim.x;
 
-  // state slot of tile (sequence n, v-head h); under continuous batching a
-  // slot outside the pool marks a padding sequence, left untouched
+  // state slot a tile (sequence n, v-head h) starts from; under continuous
+  // batching a slot outside the pool marks a padding sequence, left
+  // untouched.  Speculative decoding (slot_stride > 0): the slots of sequence
+  // n are row n of a [N][slot_stride] table, the state after token t goes to
+  // entry t, and the initial state is entry accepted[n] - 1 (entry 0 without
+  // `accepted`), the state after the last accepted token of the previous step.
   auto slot_of = [&](int tile) {
     const int n = tile / Hv;
     int slot = n;
     if (slots) {
-      slot = slots[n];
+      int col = 0;
+      if (slot_stride > 0 && accepted) {
+        col = accepted[n] - 1;
+        if (col < 0 || col >= slot_stride) return -1;
+      }
+      slot = slots[(size_t)n * (slot_stride > 0 ? slot_stride : 1) + col];
       if (slot < 0 || slot >= num_slots) slot = -1;
     }
     return slot;
@@ -109,6 +119,12 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     }
     for (int t = s; t < e; ++t) {
       const size_t qk_row = ((size_t)t * Hqk + hq) * K;
+      // speculative decoding: slot receiving the state after this token
+      int tslot = -1;
+      if (slot_stride > 0 && t - s < slot_stride) {
+        tslot = slots[(size_t)n * slot_stride + (t - s)];
+        if (tslot >= num_slots) tslot = -1;
+      }
       if (tid < K) {
         kq_s[0][tid] = bf2f(k[qk_row + tid]);
         kq_s[1][tid] = bf2f(q[qk_row + tid]);
@@ -177,8 +193,14 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
         for (int c = 0; c < 4; ++c) ob[c] = f2bf(ov[c]);
         *reinterpret_cast<u16x4*>(o + vh * V + 4 * cg) = ob;
       }
+      if (ht && tslot >= 0) {
+        f32x4* dst = reinterpret_cast<f32x4*>(ht + ((size_t)tslot * Hv + h) * (size_t)K * V);
+#pragma unroll
+        for (int i = 0; i < RPT; ++i)
+          __builtin_nontemporal_store(S[i], dst + (size_t)(rg + ROWG * i) * COLG + cg);
+      }
     }
-    if (ht) {
+    if (ht && slot_stride == 0) {
       f32x4* dst = reinterpret_cast<f32x4*>(ht + ((size_t)slot * Hv + h) * (size_t)K * V);
 #pragma unroll
       for (int i = 0; i < RPT; ++i)
@@ -207,7 +229,8 @@ static void launch_recurrent(const uint16_t* q, const uint16_t* k, const uint16_
                              const float* g, const float* beta, const float* h0,
                              float* ht, uint16_t* o, const int32_t* cu, int B, int T,
                              int Hqk, int Hv, int N, float scale, int l2norm,
-                             const int32_t* slots, int num_slots, hipStream_t stream) {
+                             const int32_t* slots, int num_slots, hipStream_t stream,
+                             int slot_stride = 0, const int32_t* accepted = nullptr) {
   const int total_tokens = B * T;
   constexpr int NT = (K * V >= 128 * 128) ? 512 : 256;
   const int ntiles = N * Hv;
@@ -216,7 +239,7 @@ static void launch_recurrent(const uint16_t* q, const uint16_t* k, const uint16_
   const int grid = ntiles < kDecodeGrid ? ntiles : kDecodeGrid;
   hipLaunchKernelGGL((recurrent_kernel<K, V, NT>), dim3(grid), dim3(NT), 0, stream, q, k, v,
                      g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm, slots,
-                     num_slots, ntiles);
+                     num_slots, ntiles, slot_stride, accepted);
 }
 
 }  // namespace gdn
@@ -295,4 +318,48 @@ extern "C" int gdn_recurrent_fwd_indexed(const void* q, const void* k, const voi
   GDN_RECI(64, 128)
 #undef GDN_RECI
   return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_indexed: unsupported K/V");
+}
+
+// Speculative decoding over a state pool (declared in gdn_layer.h): per-token
+// states into the slots of a [N, index_stride] table, the initial state from
+// the slot of the last accepted token.
+extern "C" int gdn_recurrent_fwd_spec(const void* q, const void* k, const void* v,
+                                      const float* g, const float* beta, float* pool, void* o,
+                                      const int32_t* cu_seqlens, const int32_t* state_indices,
+                                      int index_stride, const int32_t* num_accepted_tokens,
+                                      int B, int T, int Hqk, int Hv, int K, int V, int N,
+                                      int num_slots, float scale, int use_qk_l2norm,
+                                      void* stream) {
+  int rc = gdn_host::validate_common(q, k, v, g, beta, nullptr, nullptr, o, cu_seqlens, B, T,
+                                     Hqk, Hv, K, V, N);
+  if (rc) return rc;
+  if (num_slots < 0)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_spec: num_slots must be >= 0");
+  if (index_stride <= 0)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_spec: index_stride must be > 0");
+  if (!cu_seqlens && T > index_stride)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_spec: T (" + std::to_string(T) +
+                                             ") exceeds index_stride (" +
+                                             std::to_string(index_stride) + ")");
+  if (N > 0 && (!state_indices || !pool))
+    return gdn_host::fail(GDN_ERR_NULL, "gdn_recurrent_fwd_spec: pool and state_indices must be non-NULL");
+  if (N == 0 || num_slots == 0 || (long long)B * T == 0) return GDN_OK;
+  auto* qq = static_cast<const uint16_t*>(q);
+  auto* kk = static_cast<const uint16_t*>(k);
+  auto* vv = static_cast<const uint16_t*>(v);
+  auto* oo = static_cast<uint16_t*>(o);
+  auto st = static_cast<hipStream_t>(stream);
+#define GDN_RECS(KK, VV)                                                                    \
+  if (K == KK && V == VV) {                                                                 \
+    gdn::launch_recurrent<KK, VV>(qq, kk, vv, g, beta, pool, pool, oo, cu_seqlens, B, T, Hqk, \
+                                  Hv, N, scale, use_qk_l2norm, state_indices, num_slots, st, \
+                                  index_stride, num_accepted_tokens);                       \
+    return gdn_host::check_launch("gdn_recurrent_fwd_spec");                                \
+  }
+  GDN_RECS(128, 128)
+  GDN_RECS(64, 64)
+  GDN_RECS(128, 64)
+  GDN_RECS(64, 128)
+#undef GDN_RECS
+  return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_spec: unsupported K/V");
 }

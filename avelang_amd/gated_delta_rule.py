@@ -381,6 +381,7 @@ def fused_recurrent_gated_delta_rule(
     use_qk_l2norm_in_kernel: bool = False,
     inplace_final_state: bool = True,
     ssm_state_indices: Optional[torch.Tensor] = None,
+    num_accepted_tokens: Optional[torch.Tensor] = None,
     *,
     out: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
@@ -399,8 +400,23 @@ def fused_recurrent_gated_delta_rule(
     slot is updated in place and the pool returned.  A slot outside
     ``[0, num_slots)`` marks a padding sequence: its state is untouched and
     its output rows are left unwritten.  Sequences must use distinct slots.
+
+    Speculative decoding: with a 2-D ``ssm_state_indices`` (int32 [N, S]) the
+    state after token t of sequence n is written to slot
+    ``ssm_state_indices[n, t]`` (t < S; an entry outside the pool skips that
+    write), so the states after every draft token are kept and a rejected
+    draft is rolled back by starting the next step from the slot of the last
+    accepted token: ``num_accepted_tokens`` (int32 [N]) selects the initial
+    slot ``ssm_state_indices[n, num_accepted_tokens[n] - 1]`` (default entry
+    0).  The pool is updated in place and returned.
     """
     name = "fused_recurrent_gated_delta_rule"
+    if ssm_state_indices is not None and ssm_state_indices.dim() == 2:
+        return _recurrent_spec(q, k, v, g, beta, scale, initial_state, cu_seqlens,
+                               use_qk_l2norm_in_kernel, inplace_final_state, ssm_state_indices,
+                               num_accepted_tokens, out, name)
+    if num_accepted_tokens is not None:
+        raise ValueError(f"{name}: num_accepted_tokens requires a 2-D ssm_state_indices [N, S].")
     if ssm_state_indices is not None:
         return _recurrent_indexed(q, k, v, g, beta, scale, initial_state, output_final_state,
                                   cu_seqlens, use_qk_l2norm_in_kernel, inplace_final_state,
@@ -448,8 +464,11 @@ def _recurrent_indexed(q, k, v, g, beta, scale, pool, output_final_state, cu_seq
         raise ValueError(f"{name}: the state pool must be a contiguous fp32 tensor "
                          f"[num_slots, {Hv}, {K}, {V}] on {dev}.")
     if (not isinstance(idx, torch.Tensor) or tuple(idx.shape) != (N,)
-            or idx.dtype != torch.int32 or idx.device != dev):
-        raise ValueError(f"{name}: ssm_state_indices must be int32 of shape ({N},) on {dev}.")
+            or idx.dtype != torch.int32 or idx.device not in (dev, torch.device("cpu"))):
+        raise ValueError(f"{name}: ssm_state_indices must be int32 of shape ({N},) on {dev} "
+                         "or the CPU.")
+    _check_distinct_slots(idx, pool.shape[0], name)
+    idx = idx.to(dev)
     if scale is None:
         scale = K ** -0.5
     o = torch.empty_like(v) if out is None else out
@@ -463,3 +482,54 @@ def _recurrent_indexed(q, k, v, g, beta, scale, pool, output_final_state, cu_seq
         int(bool(use_qk_l2norm_in_kernel)), _stream_ptr(dev))
     _native.check(rc, name)
     return o, ht
+
+
+def _check_distinct_slots(idx: torch.Tensor, num_slots: int, name: str) -> None:
+    """Reject a host-resident slot table that gives two sequences the same slot
+    (their state updates would race); device tables are the caller's contract."""
+    if idx.device.type != "cpu":
+        return
+    valid = idx[(idx >= 0) & (idx < num_slots)]
+    if valid.numel() != torch.unique(valid).numel():
+        raise ValueError(f"{name}: ssm_state_indices uses a slot more than once.")
+
+
+def _recurrent_spec(q, k, v, g, beta, scale, pool, cu_seqlens, use_qk_l2norm_in_kernel,
+                    inplace_final_state, idx, accepted, out, name):
+    if pool is None or not isinstance(pool, torch.Tensor) or pool.dim() != 4:
+        raise ValueError(f"{name}: a 2-D ssm_state_indices requires initial_state as a state "
+                         "pool [num_slots, Hv, K, V].")
+    if not inplace_final_state:
+        raise ValueError(f"{name}: with ssm_state_indices the states are written in place.")
+    q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
+        q, k, v, g, beta, None, cu_seqlens, name)
+    dev = q.device
+    if (tuple(pool.shape[1:]) != (Hv, K, V) or pool.dtype != torch.float32
+            or pool.device != dev or not pool.is_contiguous()):
+        raise ValueError(f"{name}: the state pool must be a contiguous fp32 tensor "
+                         f"[num_slots, {Hv}, {K}, {V}] on {dev}.")
+    if (not isinstance(idx, torch.Tensor) or idx.dim() != 2 or idx.shape[0] != N
+            or idx.dtype != torch.int32):
+        raise ValueError(f"{name}: a 2-D ssm_state_indices must be int32 of shape ({N}, S).")
+    if cu is None and T > idx.shape[1]:
+        raise ValueError(f"{name}: T ({T}) exceeds the ssm_state_indices row length "
+                         f"({idx.shape[1]}).")
+    _check_distinct_slots(idx, pool.shape[0], name)
+    idx = idx.to(dev).contiguous()
+    if accepted is not None:
+        if (not isinstance(accepted, torch.Tensor) or tuple(accepted.shape) != (N,)
+                or accepted.dtype != torch.int32):
+            raise ValueError(f"{name}: num_accepted_tokens must be int32 of shape ({N},).")
+        accepted = accepted.to(dev).contiguous()
+    if scale is None:
+        scale = K ** -0.5
+    o = torch.empty_like(v) if out is None else out
+    if o.shape != v.shape or o.dtype != torch.bfloat16 or o.device != dev or not o.is_contiguous():
+        raise ValueError(f"{name}: out must be a contiguous bf16 tensor of shape {tuple(v.shape)}.")
+    rc = _native.lib().gdn_recurrent_fwd_spec(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+        pool.data_ptr(), o.data_ptr(), _ptr(cu), idx.data_ptr(), idx.shape[1], _ptr(accepted),
+        B, T, Hqk, Hv, K, V, N, pool.shape[0], float(scale),
+        int(bool(use_qk_l2norm_in_kernel)), _stream_ptr(dev))
+    _native.check(rc, name)
+    return o, pool

@@ -70,6 +70,11 @@ def decode_bytes(N, Hqk, Hv, K=128, V=128):
     return 2 * N * Hv * K * V * 4 + N * (2 * Hqk * K + 2 * Hv * V) * 2 + N * Hv * 2 * 4
 
 
+TRAFFIC_SOURCE = ("profiles/traffic.json: HBM bytes per launch from two rocprofv3 --pmc runs "
+                  "(FETCH_SIZE, WRITE_SIZE) of bench.py --profile-pass, each scaled by a 256 MiB "
+                  "copy in the same run (bench.py --pmc-summary); not measured in this run")
+
+
 def _load_traffic(name):
     """HBM bytes per launch measured by rocprofv3 --pmc (profiles/traffic.json), if present."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -187,10 +192,17 @@ def cpu_backward(wl, runs=3):
                        initial_state=a["initial_state"], dtype=np.float32)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
+    from oracle import cpu as oracle
+
     threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    host = oracle.host_info(threads)
+    host["compiler"], host["cflags"] = "numpy (BLAS)", None
     return dict(value=T / med, unit="tokens/s", cores=threads, kind="port",
+                implementation="numpy",
                 sample=f"config 1 in full (T={T}, {Hv} v-heads), numpy fp32 chunked backward "
-                       f"oracle, median of {runs} runs ({med:.2f} s each)")
+                       f"oracle (oracle/gdn_bwd_ref.py; threads = the BLAS pool's), median of "
+                       f"{runs} runs ({med:.2f} s each)",
+                host=host)
 
 
 def bench_prefill_config(dev, name, reps=3):
@@ -352,7 +364,7 @@ def bench_layer_ops(dev):
 def cpu_prefill(wl, runs=5):
     from oracle import cpu as oracle
 
-    threads = oracle.default_threads()
+    threads = oracle.host_threads()
     a = wl.numpy()
     oracle.run("chunk", **a, threads=threads)          # warm-up
     times = []
@@ -363,14 +375,16 @@ def cpu_prefill(wl, runs=5):
     med = float(np.median(times))
     return dict(value=wl.dims["T"] / med, unit="tokens/s", cores=threads, kind="port",
                 sample=f"config 1 in full (T={wl.dims['T']}, 32 v-heads), C/OpenMP fp32 "
-                       f"chunked oracle, median of {runs} runs ({med * 1e3:.1f} ms each)")
+                       f"chunked oracle (oracle/gdn_cpu.c), median of {runs} runs "
+                       f"({med * 1e3:.1f} ms each)",
+                host=oracle.host_info(threads))
 
 
 def cpu_decode(runs=3):
     from avelang_amd import workloads as W
     from oracle import cpu as oracle
 
-    threads = oracle.default_threads()
+    threads = oracle.host_threads()
     wl = W.config("cfg2_decode_b256", seed=200)
     a = wl.numpy()
     d = wl.dims
@@ -383,7 +397,9 @@ def cpu_decode(runs=3):
     med = float(np.median(times))
     nb = decode_bytes(d["N"], d["Hqk"], d["Hv"], d["K"], d["V"])
     return dict(value=nb / med / 1e9, unit="GB/s", cores=threads, kind="port",
-                sample=f"one full config-2 decode step (256 x 32 state tiles), median of {runs}")
+                sample=f"one full config-2 decode step (256 x 32 state tiles), C/OpenMP fp32 "
+                       f"recurrence (oracle/gdn_cpu.c), median of {runs}",
+                host=oracle.host_info(threads))
 
 
 def profile_pass(dev, reps=3, what="all"):
@@ -542,6 +558,7 @@ def _backward_record(bwd, no_cpu):
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                      "traffic": _load_traffic("backward"),
+                     "traffic_source": TRAFFIC_SOURCE,
                      "kernel": "gdn_chunk_bwd = chunk_prep<bwd> + chunk_chain<save> + "
                                "chunk_rev + chunk_grad",
                      "algorithmic_flops_per_launch": flops,
@@ -640,6 +657,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": _load_traffic("prefill"),
+                     "traffic_source": TRAFFIC_SOURCE,
                      "kernel": "gdn_chunk_fwd = chunk_prep + chunk_chain (+ chunk_table with cu_seqlens)",
                      "algorithmic_flops_per_launch": flops,
                      "flops_per_token_per_vhead": 6 * C * pre["K"] + 4 * C * pre["V"] + 6 * pre["K"] * pre["V"]},
@@ -651,6 +669,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
                          "traffic": _load_traffic("decode"),
+                     "traffic_source": TRAFFIC_SOURCE,
                          "kernel": "recurrent_kernel<128,128>",
                          "algorithmic_bytes_per_launch": dec["bytes"]},
             "cpu_baseline": cpu_dec,

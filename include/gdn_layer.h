@@ -121,6 +121,33 @@ int gdn_recurrent_fwd_indexed(const void* q, const void* k, const void* v,
                               int B, int T, int Hqk, int Hv, int K, int V, int N,
                               int num_slots, float scale, int use_qk_l2norm, void* stream);
 
+/*
+ * Speculative-decoding step over a state pool (draft tokens verified in one
+ * call; the convention of the serving call site of fused_recurrent_gated_
+ * delta_rule with a 2-D ssm_state_indices and num_accepted_tokens).
+ *   state_indices        [N, index_stride] int32: the state after token t
+ *                        (0-based within sequence n, t < index_stride) is
+ *                        written to slot state_indices[n][t]; an entry outside
+ *                        [0, num_slots) skips that write.
+ *   num_accepted_tokens  [N] int32, nullable: sequence n starts from slot
+ *                        state_indices[n][num_accepted_tokens[n] - 1] (the
+ *                        state after the last draft token the previous step
+ *                        accepted); NULL starts from state_indices[n][0].  An
+ *                        initial slot outside the pool (or an accepted count
+ *                        outside [1, index_stride]) marks a padding sequence:
+ *                        nothing of it is read or written.
+ *   pool                 [num_slots, Hv, K, V] fp32, read and written in place.
+ * Without cu_seqlens every sequence has T tokens and T <= index_stride is
+ * required; with cu_seqlens, tokens past index_stride advance the state
+ * without writing it.  Sequences must not share slots.
+ */
+int gdn_recurrent_fwd_spec(const void* q, const void* k, const void* v,
+                           const float* g, const float* beta, float* pool, void* o,
+                           const int32_t* cu_seqlens, const int32_t* state_indices,
+                           int index_stride, const int32_t* num_accepted_tokens,
+                           int B, int T, int Hqk, int Hv, int K, int V, int N,
+                           int num_slots, float scale, int use_qk_l2norm, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,10 +34,61 @@ def lib():
 
 
 def default_threads() -> int:
+    """Thread count for checker runs in tests (OMP_NUM_THREADS, else at most 16)."""
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
         return max(1, int(env))
     return max(1, min(16, os.cpu_count() or 1))
+
+
+def host_threads() -> int:
+    """Every core this process may run on (the timed CPU baseline uses them all)."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:  # pragma: no cover - non-Linux
+        return max(1, os.cpu_count() or 1)
+
+
+def host_info(threads: int) -> dict:
+    """The host facts a CPU-baseline record carries: nproc, the cores this
+    process may use, physical cores, the /proc/cpuinfo model, the thread
+    count used, and the compiler and flags of the timed library."""
+    import subprocess
+
+    from . import build as _b
+
+    model, phys = None, set()
+    try:
+        pid = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and model is None:
+                    model = val
+                elif key == "physical id":
+                    pid = val
+                elif key == "core id":
+                    core = val
+                elif not key and pid is not None and core is not None:
+                    phys.add((pid, core))
+                    pid = core = None
+        if pid is not None and core is not None:
+            phys.add((pid, core))
+    except OSError:
+        pass
+    try:
+        gcc = subprocess.run(["gcc", "--version"], capture_output=True, text=True,
+                             timeout=10).stdout.splitlines()[0]
+    except (OSError, subprocess.SubprocessError, IndexError):
+        gcc = "gcc (version unavailable)"
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        affinity = None
+    return {"nproc": os.cpu_count(), "cores_available": affinity,
+            "physical_cores": len(phys) or None, "cpu_model": model, "threads": threads,
+            "compiler": gcc, "cflags": " ".join(_b.CFLAGS)}
 
 
 def _f32(x):

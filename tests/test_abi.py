@@ -32,7 +32,8 @@ def test_header_declares_expected_entry_points():
                                      "gdn_last_error", "gdn_recurrent_fwd"]
     assert _declared(("gdn_layer.h",)) == [
         "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_gating_fwd",
-        "gdn_l2norm_fwd", "gdn_recurrent_fwd_indexed", "gdn_rmsnorm_gated_fwd"]
+        "gdn_l2norm_fwd", "gdn_recurrent_fwd_indexed", "gdn_recurrent_fwd_spec",
+        "gdn_rmsnorm_gated_fwd"]
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -199,7 +200,24 @@ def _reci(lib, **kw):
                                          0.1, 0, None)
 
 
+def _recs(lib, **kw):
+    p = dict(q=1 << 20, k=2 << 20, v=3 << 20, g=4 << 20, beta=5 << 20, pool=7 << 20,
+             o=6 << 20, cu=None, idx=8 << 20, stride=4, acc=None, B=2, T=4, Hqk=2, Hv=4,
+             K=128, V=128, N=2, slots=8)
+    p.update(kw)
+    return lib.gdn_recurrent_fwd_spec(p["q"], p["k"], p["v"], p["g"], p["beta"], p["pool"],
+                                      p["o"], p["cu"], p["idx"], p["stride"], p["acc"], p["B"],
+                                      p["T"], p["Hqk"], p["Hv"], p["K"], p["V"], p["N"],
+                                      p["slots"], 0.1, 0, None)
+
+
 @pytest.mark.parametrize("call,code,msg", [
+    (lambda l: _recs(l, stride=0), -2, "index_stride must be > 0"),
+    (lambda l: _recs(l, T=5), -2, "exceeds index_stride"),
+    (lambda l: _recs(l, idx=None), -1, "state_indices"),
+    (lambda l: _recs(l, pool=None), -1, "pool"),
+    (lambda l: _recs(l, slots=-1), -2, "num_slots"),
+    (lambda l: _recs(l, K=96), -2, "unsupported head sizes"),
     (lambda l: l.gdn_gating_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 8, 0,
                                 1, 1, 0, 1.0, 20.0, None), -2, "H > 0"),
     (lambda l: l.gdn_gating_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 8, 4,
@@ -247,3 +265,4 @@ def test_layer_empty_problems_launch_nothing(lib):
     assert _conv(lib, B=0) == 0
     assert _convu(lib, B=0) == 0
     assert _reci(lib, N=0, B=0) == 0
+    assert _recs(lib, N=0, B=0) == 0

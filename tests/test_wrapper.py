@@ -93,3 +93,13 @@ def test_state_pool_validation():
                                          initial_state=torch.zeros(3, 4, 128, 128),
                                          output_final_state=True, inplace_final_state=False,
                                          ssm_state_indices=torch.zeros(2, dtype=torch.int32))
+
+
+def test_host_slot_table_rejects_shared_slots():
+    from avelang_amd.gated_delta_rule import _check_distinct_slots
+    _check_distinct_slots(torch.tensor([0, 2, -1, -1, 5], dtype=torch.int32), 6, "op")
+    _check_distinct_slots(torch.tensor([[0, 1], [2, 9]], dtype=torch.int32), 6, "op")
+    with pytest.raises(ValueError, match="more than once"):
+        _check_distinct_slots(torch.tensor([0, 2, 2], dtype=torch.int32), 6, "op")
+    with pytest.raises(ValueError, match="more than once"):
+        _check_distinct_slots(torch.tensor([[0, 1], [1, 3]], dtype=torch.int32), 6, "op")
