@@ -85,4 +85,10 @@ void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
 
 ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb);
 
+// Forward chain, state-wave form (gdn_chunk_chain.hip): o and ht only.
+template <int K>
+void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
+                     float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
+                     int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st);
+
 }  // namespace gdn

@@ -833,9 +833,13 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
     hipLaunchKernelGGL((chunk_prep_kernel<K, BWD>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0,
                        st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised
-  hipLaunchKernelGGL((chunk_chain_kernel<K, BWD, OUT>), dim3(N * Hv * (V / 16)), dim3(256), 0, st,
-                     l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
-                     OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  if constexpr (OUT && !BWD)
+    launch_chain_sw<K>(l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V,
+                       scale, ws, st);
+  else
+    hipLaunchKernelGGL((chunk_chain_kernel<K, BWD, OUT>), dim3(N * Hv * (V / 16)), dim3(256), 0,
+                       st, l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
+                       OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws);
 }
 
 void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,

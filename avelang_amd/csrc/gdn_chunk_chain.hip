@@ -1,0 +1,507 @@
+// Forward chain of the chunked prefill, state-wave form (gfx950).
+//
+// One workgroup of two waves per (sequence, v-head, 16-column V tile),
+// sequential over the sequence's chunks of 64 tokens:
+//
+//   wave 0, the state wave, holds every key row of the tile's fp32 state in
+//   VGPRs and runs the serial part of a chunk step alone:
+//       X = K S,  Y = V - e^G X,  vnew = Tb Y,
+//       S = e^G_last S + K^T (e^(G_last - G) vnew)
+//   (Tb = (I + A)^-1 diag(beta) from the prep kernel; K S, Tb Y and K^T U
+//   as hi + lo bf16 MFMA products).  Each product's result tile is the next
+//   product's B operand where it stands (row orders below), so no LDS
+//   exchange and no barrier sits inside the step.
+//
+//   wave 1, the stage wave, fills LDS with chunk c+1's operands (the K rows,
+//   the Tb fragments, the V tile as fp32 in the state wave's layout, e^G
+//   and e^(G_last - G))
+//   and forms chunk c-1's output from the state and vnew fragments the state
+//   wave leaves in LDS:  o = scale e^G (Q S) + P vnew.
+//
+// One s_barrier per chunk step hands the buffers over (two stage buffers,
+// two output buffers).  The state wave issues no global load at all.
+//
+// Row orders.  An MFMA result tile puts rows 4 grp + r (r < 4) in lane
+// (n, grp); a B operand of k-block b takes reduction slots 8 grp + i (i < 8)
+// from lane (n, grp).  Tile row 16 T + 4 grp + r stands for index
+//     rho(16 T + 4 grp + r) = 32 (T / 2) + 8 grp + 4 (T % 2) + r,
+// so a lane's rows of tiles 2b and 2b + 1 are exactly the natural indices
+// 32 b + 8 grp + i of k-block b.  The state's key rows and the token rows of
+// X, Y and vnew use rho; K, Q, P and the columns of Tb stay in natural
+// order (the Tb fragments are gathered by rho-permuted row).
+#include <type_traits>
+
+#include "gdn_chunk.h"
+
+namespace gdn {
+
+// rho of tile row 16 T + m (m < 16)
+__device__ __forceinline__ int rho_row(int T, int m) {
+  return 32 * (T >> 1) + 8 * (m >> 2) + 4 * (T & 1) + (m & 3);
+}
+
+__device__ __forceinline__ u16x8 cat8(u16x4 a, u16x4 b) {
+  return u16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Tb fragment slot of (row tile ti, k-block b): row tiles 0 and 1 have no
+// k-block 1 (Tb is lower triangular), so six slots per hi / lo part.
+__device__ __forceinline__ constexpr int tb_slot(int ti, int b) { return b == 0 ? ti : 2 + ti; }
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n
+// vector-memory operations are outstanding, and for nothing else.
+__device__ __forceinline__ constexpr int vmcnt_imm(int n) {
+  return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14);
+}
+
+// Staged K rows: row stride 2K + 16 bytes and 64 more bytes after every 16
+// rows.  The column-fragment reads of the state wave (16 rows rho(16 ti +
+// m), one 16-byte piece) then fall on distinct banks, and every K read is a
+// per-lane base plus a compile-time offset.
+template <int K>
+struct KLayout {
+  static constexpr int RS = 2 * K + 16;            // row stride (bytes)
+  static constexpr int GP = 64;                    // extra bytes per 16 rows
+  static constexpr int GU = (16 * RS + GP) / 16;   // 16-byte units per 16 rows
+  static constexpr int UNITS = 4 * GU;             // units of the 64 rows
+  static constexpr int LOADS = (UNITS + 63) / 64;  // 1 KiB direct-to-LDS loads
+  static constexpr int BYTES = LOADS * 1024;       // buffer size
+  __device__ static constexpr int row(int r) { return r * RS + (r >> 4) * GP; }
+};
+
+template <int K>
+__global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
+    const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
+    float scale, ChunkWs ws) {
+  constexpr int KB = K / 32;   // k-blocks over the key index
+  constexpr int ST = K / 16;   // 16-row state tiles
+  // Stage buffers (chunk c in buffer c % 3): the chunk's K rows (KLayout),
+  // the Tb A fragments in rho row order, the V tile as fp32 in the state
+  // wave's layout (lane (n16, grp) of token tile ti reads
+  // Vst[.][ti][grp][4 n16 ..]; the padded rows put the stage wave's
+  // scattered writes on distinct banks), e^G and e^(G_last - G) by token,
+  // and e^G_last.
+  using KL = KLayout<K>;
+  __shared__ __attribute__((aligned(16))) unsigned char Kst[3][KL::BYTES];
+  __shared__ __attribute__((aligned(16))) u16x8 Tst[3][6][2][64];
+  __shared__ __attribute__((aligned(16))) float Vst[3][4][4][68];
+  __shared__ __attribute__((aligned(16))) float Gst[3][2][64];
+  __shared__ float Egl[3];
+  // Output buffers (chunk c in buffer c % 3), left by the state wave for
+  // the output wave: the state's hi B fragments at the chunk start and
+  // vnew (bf16) as B fragments.
+  __shared__ __attribute__((aligned(16))) u16x8 Sx[3][KB][64];
+  __shared__ __attribute__((aligned(16))) u16x8 Vx[3][2][64];
+
+  const int NVT = V / 16;
+  // XCD-aware placement, as in the four-wave chain: a qk-head group's
+  // workgroups stay on one XCD (shared K / Q / Tb / P in its L2), and the
+  // groups are dealt round-robin so every XCD gets a share of each sequence.
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  const int unit = NVT * (Hv / Hqk);
+  if (nb % (8 * unit) == 0) {
+    const int i = bid >> 3;
+    bid = ((i / unit) * 8 + (bid & 7)) * unit + i % unit;
+  } else if ((nb & 7) == 0) {
+    bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  }
+  const int vt = bid % NVT;
+  const int h = (bid / NVT) % Hv;
+  const int n = bid / NVT / Hv;
+  const int hq = h / (Hv / Hqk);
+
+  const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int r16 = lane % 16, grp = lane / 16;
+
+  int s, e;
+  seq_bounds(cu, n, T, total, s, e);
+  const int nct = (T + kChunk - 1) / kChunk;
+  const int c_begin = cu ? ws.off[n] : n * nct;
+  const int nc = (cu ? ws.off[n + 1] : (n + 1) * nct) - c_begin;
+
+  if (w == 0) {
+    // ------------------------------------------------------ state wave ----
+    // state tile t: lane (n16, grp), element r = S[rho(16t + 4grp + r)][16 vt + n16]
+    const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
+    f32x4 S[ST];
+    if (h0) {
+#pragma unroll
+      for (int t = 0; t < ST; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[t][r] = h0[tile + (size_t)rho_row(t, 4 * grp + r) * V];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < ST; ++t) S[t] = zero4();
+    }
+    __syncthreads();   // stage buffer 0 is filled
+
+    // per-lane byte offsets into a K stage buffer: K A fragments (row
+    // rho(16 ti + r16), piece grp; k-block b adds 64 b) and the transposing
+    // reads of K^T (rows 8 grp + m4 and 8 grp + 4 + m4, piece q4; k-block b
+    // adds 32 rows, state tile t adds 4 (t / 2) pieces and 8 (t % 2) bytes)
+    const int m4 = r16 >> 2, q4 = r16 & 3;
+    int ka_off[4];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) ka_off[ti] = KL::row(rho_row(ti, r16)) + 16 * grp;
+    const int tr_lo = KL::row(8 * grp + m4) + 16 * q4;
+    const int tr_hi = KL::row(8 * grp + 4 + m4) + 16 * q4;
+
+    // one chunk step on stage / output buffer B3 (a compile-time index, so
+    // that every LDS address is a per-lane base plus an immediate)
+    auto step = [&](auto b3c) {
+      constexpr int b3 = decltype(b3c)::value;
+      const unsigned char* Kb = Kst[b3];
+      // operands of the step, all from LDS and issued first
+      u16x8 ka[KB][4], ta[6][2];
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+          ka[b][ti] = *reinterpret_cast<const u16x8*>(Kb + ka_off[ti] + 64 * b);
+      }
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        ta[i][0] = Tst[b3][i][0][lane];
+        ta[i][1] = Tst[b3][i][1][lane];
+      }
+      f32x4 eg[4], dc[4], vv[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int r0 = 32 * (ti >> 1) + 8 * grp + 4 * (ti & 1);
+        eg[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][0][r0]);
+        dc[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][1][r0]);
+        vv[ti] = *reinterpret_cast<const f32x4*>(&Vst[b3][ti][grp][4 * r16]);
+      }
+      const float egl = Egl[b3];
+
+      // X = K S on the four rho-ordered token tiles, k-block by k-block:
+      // the split of state tiles 2b, 2b+1 feeds k-block b
+      f32x4 X[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) X[ti] = zero4();
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        u16x4 h0v, l0v, h1v, l1v;
+        split_bf4(S[2 * b], h0v, l0v);
+        split_bf4(S[2 * b + 1], h1v, l1v);
+        const u16x8 sh = cat8(h0v, h1v), sl = cat8(l0v, l1v);
+        Sx[b3][b][lane] = sh;   // for this chunk's Q S (output wave)
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sh, X[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sl, X[ti]);
+      }
+      // Y = V - e^G X (B fragments, hi and lo) and vnew = Tb Y, k-block 0
+      // first: row tiles 0 and 1 of vnew are then complete
+      auto ysplit = [&](int b, u16x8& yh, u16x8& yl) {
+        u16x4 hh0, ll0, hh1, ll1;
+        split_bf4(vv[2 * b] - eg[2 * b] * X[2 * b], hh0, ll0);
+        split_bf4(vv[2 * b + 1] - eg[2 * b + 1] * X[2 * b + 1], hh1, ll1);
+        yh = cat8(hh0, hh1);
+        yl = cat8(ll0, ll1);
+      };
+      f32x4 vn[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) vn[ti] = zero4();
+      {
+        u16x8 yh, yl;
+        ysplit(0, yh, yl);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 0)][0], yh, vn[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 0)][0], yl, vn[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 0)][1], yh, vn[ti]);
+      }
+      // K^T fragments of the update: element i of lane (m, grp) for state
+      // tile t, k-block b is K[32 b + 8 grp + i][rho(16 t + m)], two
+      // transposing reads of 4 token rows each
+      u16x8 kt[2][ST];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int t = 0; t < ST; ++t) {
+          const int imm = KL::row(32 * b) + 64 * (t >> 1) + 8 * (t & 1);
+          const u16x4 lo4 = lds_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_lo + imm));
+          const u16x4 hi4 = lds_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_hi + imm));
+          kt[b][t] = cat8(lo4, hi4);
+        }
+      }
+      {
+        u16x8 yh, yl;
+        ysplit(1, yh, yl);
+#pragma unroll
+        for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 1)][0], yh, vn[ti]);
+#pragma unroll
+        for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 1)][0], yl, vn[ti]);
+#pragma unroll
+        for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 1)][1], yh, vn[ti]);
+      }
+      // U = e^(G_last - G) vnew (hi, lo) and vnew (bf16) for the output;
+      // S = e^G_last S + K^T U, k-block by k-block
+#pragma unroll
+      for (int t = 0; t < ST; ++t) S[t] = S[t] * egl;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        u16x4 hh0, ll0, hh1, ll1;
+        split_bf4(dc[2 * b] * vn[2 * b], hh0, ll0);
+        split_bf4(dc[2 * b + 1] * vn[2 * b + 1], hh1, ll1);
+        const u16x8 uh = cat8(hh0, hh1), ul = cat8(ll0, ll1);
+        Vx[b3][b][lane] = cat8(f2bf4(vn[2 * b]), f2bf4(vn[2 * b + 1]));
+#pragma unroll
+        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], uh, S[t]);
+#pragma unroll
+        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], ul, S[t]);
+      }
+      __syncthreads();   // chunk c's outputs published; stage buffer c % 3 free
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    int c = 0;
+    for (; c + 2 < nc; c += 3) {
+      step(I0{});
+      step(I1{});
+      step(I2{});
+    }
+    if (c < nc) step(I0{});
+    if (c + 1 < nc) step(I1{});
+    if (ht) {
+#pragma unroll
+      for (int t = 0; t < ST; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ht[tile + (size_t)rho_row(t, 4 * grp + r) * V] = S[t][r];
+      }
+    }
+  } else if (w == 1) {
+    // ------------------------------------------------------ stage wave ----
+    // Issues chunk j+2's K rows and Tb fragments straight to LDS during step
+    // j (buffer_load ... lds: 16 bytes per lane, 1 KiB per instruction, lane
+    // l to bytes 16 l of the block) and, before the step's barrier, waits
+    // for chunk j+1's, issued during step j-1.  The wave writes LDS in no
+    // other way: the compiler would wait for every load in flight before
+    // such a write.  Its barriers are bare s_barriers (a workgroup release
+    // fence would wait for the loads still in flight for the next step),
+    // with signal fences so that no LDS access moves across them.
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    constexpr int P = K / 8;             // 16-byte pieces per K row
+    constexpr int kKT = KL::LOADS + 12;  // loads per stage: K blocks + Tb fragments
+    const int rowq = Hqk * K * 2;   // byte stride of a K row
+    // chunk j's data into buffer jb % 3 (past the last chunk the loads repeat
+    // it into a buffer no step reads, which keeps every step's count equal)
+    auto issue_kt = [&](int j, int jb) {
+      const int ci = c_begin + j, buf = jb % 3;
+      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+      // K rows in KLayout: 16-byte unit p = 64 i + lane of the buffer is a
+      // piece of a row or padding (padding reads out of range, as 0); rows
+      // >= L read as 0
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(k + ((size_t)t0 * Hqk + hq) * K), 0, L * rowq, kBufferFlags);
+#pragma unroll
+      for (int i = 0; i < KL::LOADS; ++i) {
+        const int p = 64 * i + lane;
+        const int g16 = p / KL::GU, rem = p % KL::GU;
+        const int row = 16 * g16 + rem / (KL::RS / 16), piece = rem % (KL::RS / 16);
+        const bool data = rem < 16 * (KL::RS / 16) && piece < P && p < KL::UNITS;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(Kst[buf] + 1024 * i), 16,
+                                                 data ? row * rowq + 16 * piece : 0x7ffffff0,
+                                                 0, 0, 0);
+      }
+      // Tb fragments gathered by rho row from the prep's natural fragments
+      const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+          ws.tfrag + ((size_t)ci * Hv + h) * 4 * 256, 0, 4 * 256 * 16, kBufferFlags);
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int row = rho_row(ti, r16);
+        const int src = (row >> 4) * 256 + (row & 15) + 16 * grp;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          if (b == 1 && ti < 2) continue;
+#pragma unroll
+          for (int hl = 0; hl < 2; ++hl)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr)&Tst[buf][tb_slot(ti, b)][hl][0],
+                                                     16, (src + 128 * b + 64 * hl) * 16, 0, 0, 0);
+        }
+      }
+    };
+    auto barrier = [] {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    };
+    if (nc > 0) {
+      issue_kt(0, 0);
+      issue_kt(min(1, nc - 1), 1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // chunk 0
+    }
+    barrier();
+    for (int j = 0; j < nc; ++j) {
+      issue_kt(min(j + 2, nc - 1), j + 2);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // chunk j+1
+      barrier();
+    }
+  } else {
+    // ----------------------------------------------------- output wave ----
+    // During step j: writes chunk j+1's V tile (as fp32, in the state wave's
+    // layout) and gate factors into stage buffer (j+1) % 3, forms chunk
+    // j-1's output, then loads chunk j+1's Q rows and P fragments and chunk
+    // j+3's V tile and G into registers.  A register set is loaded two
+    // steps before it is used (two sets, the loop unrolled by two), and
+    // every step issues the same loads and stores, so each wait names an
+    // exact count.
+    constexpr int kQP = 4 * KB + 6;      // Q / P loads per chunk
+    constexpr int kVG = 3;               // V tile (2) + G (1)
+    constexpr int kStep = 4 + kQP + kVG; // output stores + loads per step
+    const int rowq = Hqk * K * 2;
+    struct Regs {
+      u16x8 qf[4][KB];   // Q rows 16 ti + r16, B operand of (Q S)^T
+      u16x8 pf[6];       // P fragments by tb_slot
+      u16x8 v0, v1;      // V tile row `lane`, 16 columns
+      float G;           // G of token `lane`
+    };
+    Regs rA, rB;
+    auto load_qp = [&](Regs& r, int j) {
+      const int ci = c_begin + j;
+      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+      const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(q + ((size_t)t0 * Hqk + hq) * K), 0, L * rowq, kBufferFlags);
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+          r.qf[ti][b] = __builtin_bit_cast(
+              u16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                         rq, (16 * ti + r16) * rowq + (32 * b + 8 * grp) * 2, 0, 0));
+      }
+      const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+          ws.pfrag + ((size_t)ci * Hv + h) * 4 * 128, 0, 4 * 128 * 16, kBufferFlags);
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          if (b == 1 && ti < 2) continue;
+          r.pf[tb_slot(ti, b)] = __builtin_bit_cast(
+              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (ti * 128 + b * 64 + lane) * 16, 0, 0));
+        }
+      }
+    };
+    auto load_vg = [&](Regs& r, int j) {
+      const int ci = c_begin + j;
+      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V + 16 * vt), 0,
+          (L - 1) * Hv * V * 2 + 32, kBufferFlags);
+      r.v0 = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * Hv * V * 2, 0, 0));
+      r.v1 = __builtin_bit_cast(u16x8,
+                                __builtin_amdgcn_raw_buffer_load_b128(rv, lane * Hv * V * 2 + 16, 0, 0));
+      const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(ws.gate + ((size_t)ci * Hv + h) * 64), 0, 256, kBufferFlags);
+      r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
+    };
+    auto write_vg = [&](const Regs& r, int j) {
+      const int buf = j % 3;
+      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+      // token row t = lane sits at tile ti = 2 (t / 32) + (t / 4) % 2,
+      // lane (n16, (t / 8) % 4), element t % 4 of the state wave's layout
+      const int ti = 2 * (lane >> 5) + ((lane >> 2) & 1);
+      float* dst = &Vst[buf][ti][(lane >> 3) & 3][lane & 3];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        dst[4 * c] = bf2f(r.v0[c]);
+        dst[4 * (c + 8)] = bf2f(r.v1[c]);
+      }
+      const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
+      const float eg = __expf(r.G);
+      Gst[buf][0][lane] = eg;
+      Gst[buf][1][lane] = __expf(GL - r.G);
+      if (lane == L - 1) Egl[buf] = eg;
+    };
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    // o^T tiles of chunk j: lane (r16, grp) holds token row 16 ti + r16,
+    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile).  With
+    // live = false (no chunk yet) the four stores go to an empty resource
+    // and are dropped.
+    auto output = [&](const Regs& r, int j, bool live) {
+      const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
+      const int b3 = j % 3;
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+      u16x8 sh[KB], vx[2];
+      if (live) {
+#pragma unroll
+        for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][b][lane];
+        vx[0] = Vx[b3][0][lane];
+        vx[1] = Vx[b3][1][lane];
+      }
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        u16x4 ov = {0, 0, 0, 0};
+        if (live) {
+          f32x4 qa = zero4(), qb = zero4();
+#pragma unroll
+          for (int b = 0; b < KB; b += 2) {
+            qa = mfma16(sh[b], r.qf[ti][b], qa);
+            qb = mfma16(sh[b + 1], r.qf[ti][b + 1], qb);
+          }
+          f32x4 pv = mfma16(vx[0], r.pf[tb_slot(ti, 0)], zero4());
+          if (ti >= 2) pv = mfma16(vx[1], r.pf[tb_slot(ti, 1)], pv);
+          const float egi = Gst[b3][0][16 * ti + r16];
+          ov = f2bf4((scale * egi) * (qa + qb) + pv);
+        }
+        __builtin_amdgcn_raw_buffer_store_b64(
+            __builtin_bit_cast(u32x2, ov), orsrc,
+            (((16 * ti + r16) * Hv + h) * V + 16 * vt + 4 * grp) * 2, 0, 0);
+      }
+    };
+    if (nc > 0) {
+      load_vg(rA, 0);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      write_vg(rA, 0);
+      load_vg(rB, min(1, nc - 1));
+      output(rA, 0, false);             // the stores a step issues, dropped
+      load_qp(rA, 0);
+      load_vg(rA, min(2, nc - 1));
+    }
+    __syncthreads();
+    // step j works on register set (j + 1) % 2
+    auto step = [&](int j, Regs& r) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kStep));   // chunk j-1's Q / P, chunk j+1's V / G
+      if (j + 1 < nc) write_vg(r, j + 1);
+      output(r, j - 1, j >= 1);
+      load_qp(r, min(j + 1, nc - 1));
+      load_vg(r, min(j + 3, nc - 1));
+      __syncthreads();
+    };
+    int j = 0;
+    for (; j + 1 < nc; j += 2) {
+      step(j, rB);
+      step(j + 1, rA);
+    }
+    if (j < nc) step(j, rB);
+    if (nc > 0) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      output((nc - 1) & 1 ? rB : rA, nc - 1, true);
+    }
+  }
+}
+
+template <int K>
+void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
+                     float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
+                     int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st) {
+  hipLaunchKernelGGL((chunk_chain_sw_kernel<K>), dim3(N * Hv * (V / 16)), dim3(192), 0, st, q,
+                     k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+}
+
+template void launch_chain_sw<64>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                  const float*, float*, uint16_t*, const int32_t*, int, int, int,
+                                  int, int, int, float, const ChunkWs&, hipStream_t);
+template void launch_chain_sw<128>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                   const float*, float*, uint16_t*, const int32_t*, int, int,
+                                   int, int, int, int, float, const ChunkWs&, hipStream_t);
+
+}  // namespace gdn
