@@ -85,8 +85,9 @@ void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
 
 ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb);
 
-// Forward chain, state-wave form (gdn_chunk_chain.hip): o and ht only.
-template <int K>
+// Forward chain, state-wave form (gdn_chunk_chain.hip).  SAVE: the state at
+// every chunk start and the per-token deltas for the backward; OUT: o, ht.
+template <int K, bool SAVE, bool OUT>
 void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
                      float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
                      int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st);

@@ -21,10 +21,12 @@
 //                       K K^T and Q K^T on MFMA, blocked UT inverse in fp32,
 //                       Tb (as bf16 hi+lo) and P (bf16) written as ready-made
 //                       MFMA A-operand fragments
-//   chunk_chain_kernel  one workgroup per (sequence, v-head, 16-column V
-//                       tile), sequential over that sequence's chunks; the
-//                       fp32 state slice lives in VGPRs for the whole sequence
-//                       and every product is a 16x16x32 bf16 MFMA.
+//   chunk_chain_sw_kernel (gdn_chunk_chain.hip)  one workgroup per (sequence,
+//                       v-head, 16-column V tile), sequential over that
+//                       sequence's chunks; one wave holds the fp32 state slice
+//                       in VGPRs for the whole sequence, every product is a
+//                       16x16x32 bf16 MFMA, and two more waves stage operands
+//                       and form the output.
 // Precision: the three products that feed the state (K S, Tb Y, K^T U) use
 // hi+lo bf16 splits of their fp32 operand(s); Q S and P vnew (output only)
 // use single bf16.
@@ -371,398 +373,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   }
 }
 
-// --------------------------------------------------------- chain (K2) ----
-// Operands of one chunk step for wave w (chunk rows 16w..16w+15), fetched
-// ahead in parts so the vector-memory queue never stalls a wave for long:
-// A (K rows) before the K S products, B (Tb, P fragments) and Q rows after
-// the first barrier, all one step ahead; C (V column slice, G) after the
-// second barrier, two steps ahead.
-template <int K>
-struct ChainIn {
-  static constexpr int KB = K / 32;
-  u16x8 kf[KB], qf[KB];   // K / Q rows, A operand of K S and Q S
-  u16x8 tf[2][2];         // Tb rows [k-block][hi, lo]
-  u16x8 pf[2];            // P rows [k-block]
-  uint16_t vv[4];         // V[row 4grp+r][16 vt + r16], raw bf16
-  float G;                // G of row `lane` (rows >= L repeat G_last)
-};
-
-struct ChainCtx {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  ChunkWs ws;
-  int s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane;
-  // per-lane byte offsets that do not change from chunk to chunk
-  int kq_off;     // row 16w + r16, columns 8grp.. of a K / Q row
-  int v_off;      // row 16w + 4grp, column 16vt + r16 of V
-};
-
-// Operand loads are raw buffer loads on a per-chunk resource covering the
-// chunk's L rows: rows past the sequence end read as zero (hardware bounds
-// check, no branch, no clamp), the base moves by a scalar per chunk and the
-// per-lane offsets are fixed, so a prefetch costs almost no VALU work.
-template <int K>
-__device__ __forceinline__ void chain_load_a(ChainIn<K>& in, const ChainCtx& c, int ci) {
-  const int t0 = c.s + (ci - c.c_begin) * kChunk;
-  const int L = min(kChunk, c.e - t0);
-  const size_t row0 = (size_t)t0 * c.Hqk + c.hq;
-  const int bytes = L * c.Hqk * K * 2;
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(c.k + row0 * K), 0, bytes, kBufferFlags);
-#pragma unroll
-  for (int b = 0; b < ChainIn<K>::KB; ++b)
-    in.kf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, c.kq_off + 64 * b, 0, 0));
-}
-
-// Q rows: issued after the first barrier with the Tb / P fragments, which
-// spreads the prefetch over the step (issued together with the K rows they
-// made the first phase wait on the vector-memory queue).
-template <int K>
-__device__ __forceinline__ void chain_load_q(ChainIn<K>& in, const ChainCtx& c, int ci) {
-  const int t0 = c.s + (ci - c.c_begin) * kChunk;
-  const int L = min(kChunk, c.e - t0);
-  const size_t row0 = (size_t)t0 * c.Hqk + c.hq;
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(c.q + row0 * K), 0, L * c.Hqk * K * 2, kBufferFlags);
-#pragma unroll
-  for (int b = 0; b < ChainIn<K>::KB; ++b)
-    in.qf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, c.kq_off + 64 * b, 0, 0));
-}
-
-template <int K>
-__device__ __forceinline__ void chain_load_b(ChainIn<K>& in, const ChainCtx& c, int ci) {
-  const size_t base = ((size_t)ci * c.Hv + c.h) * 4 + c.w;
-  const u16x8* tb = c.ws.tfrag + base * 256;
-  const u16x8* pb = c.ws.pfrag + base * 128;
-  in.tf[0][0] = tb[c.lane];
-  in.tf[0][1] = tb[64 + c.lane];
-  in.pf[0] = pb[c.lane];
-  // k-block 1 (columns 32..63) of row tiles 0 and 1 is zero in both Tb and
-  // P (lower triangular): those waves skip the loads (a wave-uniform branch)
-  if (c.w >= 2) {
-    in.tf[1][0] = tb[128 + c.lane];
-    in.tf[1][1] = tb[192 + c.lane];
-    in.pf[1] = pb[64 + c.lane];
-  } else {
-    const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-    in.tf[1][0] = z;
-    in.tf[1][1] = z;
-    in.pf[1] = z;
-  }
-}
-
-template <int K>
-__device__ __forceinline__ void chain_load_c(ChainIn<K>& in, const ChainCtx& c, int ci) {
-  const int t0 = c.s + (ci - c.c_begin) * kChunk;
-  const int L = min(kChunk, c.e - t0);
-  const int rowb = c.Hv * c.V * 2;
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(c.v + ((size_t)t0 * c.Hv + c.h) * c.V + 16 * c.vt), 0,
-      (L - 1) * rowb + 32, kBufferFlags);
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    in.vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, c.v_off + r * rowb, 0, 0);
-  // one 4-byte load per lane (row `lane`) instead of the per-row factors
-  // in MFMA output layout: the step forms e^G and e^(G_last - G) itself
-  in.G = c.ws.gate[((size_t)ci * c.Hv + c.h) * 64 + c.lane];
-}
-
-// SAVE: store the state at every chunk start (ws.hs) and the per-token delta
-// (ws.dl) for the backward.  OUT: write o (and ht when given).  The forward
-// is <K, false, true>, the backward's recomputation <K, true, false>, a
-// training forward that keeps what the backward needs <K, true, true>.
-template <int K, bool SAVE, bool OUT>
-__global__ __launch_bounds__(256) void chunk_chain_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
-    const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
-    float scale, ChunkWs ws) {
-  constexpr int KB = K / 32;     // k-blocks of K S
-  constexpr int RT = K / 64;     // 16-row state tiles per wave
-  constexpr int LDS_ = K + 8;    // S^T row stride (bf16)
-  constexpr int LDY = 72;        // 64-row operands
-  static_assert(KB % 2 == 0, "K S uses two accumulators per hi/lo part");
-  __shared__ __attribute__((aligned(16))) uint16_t SsT[2][16][LDS_];
-  __shared__ __attribute__((aligned(16))) uint16_t YsT[2][16][LDY];
-  __shared__ __attribute__((aligned(16))) uint16_t UsT[2][16][LDY];
-  __shared__ __attribute__((aligned(16))) uint16_t VnT[16][LDY];
-  __shared__ __attribute__((aligned(16))) uint16_t Kl[64][LDS_];
-
-  const int NVT = V / 16;
-  // Workgroups are dealt to the 8 XCDs round-robin by blockIdx.  The unit
-  // kept on one XCD is a qk-head group (its G v-heads x NVT tiles share K, Q
-  // and the Tb / P fragments through that XCD's L2), and the units are dealt
-  // round-robin too, so every XCD gets 1/8 of every sequence: with packed
-  // sequences of unequal length, contiguous ranges per XCD left some XCDs
-  // with much more work than others.
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  const int unit = NVT * (Hv / Hqk);
-  if (nb % (8 * unit) == 0) {
-    const int i = bid >> 3;
-    bid = ((i / unit) * 8 + (bid & 7)) * unit + i % unit;
-  } else if ((nb & 7) == 0) {
-    bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  }
-  const int vt = bid % NVT;
-  const int h = (bid / NVT) % Hv;
-  const int n = bid / NVT / Hv;
-  const int hq = h / (Hv / Hqk);
-
-  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
-  const int r16 = lane % 16, grp = lane / 16;
-
-  int s, e;
-  seq_bounds(cu, n, T, total, s, e);
-  const int nct = (T + kChunk - 1) / kChunk;
-  const int c_begin = cu ? ws.off[n] : n * nct, c_end = cu ? ws.off[n + 1] : (n + 1) * nct;
-  const ChainCtx ctx{q, k, v, ws, s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane,
-                     ((16 * w + r16) * Hqk * K + 8 * grp) * 2,
-                     ((16 * w + 4 * grp) * Hv * V + r16) * 2};
-
-  // state slice: rows w*16*RT + 16*tt + 4*grp + r, column 16*vt + r16
-  const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
-  f32x4 Sr[RT];
-#pragma unroll
-  for (int tt = 0; tt < RT; ++tt) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
-      Sr[tt][r] = h0 ? h0[tile + (size_t)kd * V] : 0.f;
-    }
-  }
-  auto publish_state = [&]() {
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-      u16x4 hi4, lo4;
-      split_bf4(Sr[tt], hi4, lo4);
-      const int kd0 = w * 16 * RT + 16 * tt + 4 * grp;
-      *reinterpret_cast<u16x4*>(&SsT[0][r16][kd0]) = hi4;
-      *reinterpret_cast<u16x4*>(&SsT[1][r16][kd0]) = lo4;
-    }
-  };
-  publish_state();
-  __syncthreads();
-
-  // One chunk step on `cur` (chunk ci) while `nxt` is filled for chunk cn.
-  // Every accumulation is split over independent accumulators so no MFMA
-  // chain is more than two deep (a dependent 16x16x32 MFMA costs ~34 cycles).
-  auto step = [&](ChainIn<K>& cur, ChainIn<K>& nxt, int ci, int cn, int cn2) {
-    const int t0 = s + (ci - c_begin) * kChunk;
-    const int L = min(kChunk, e - t0);
-    // SAVE: this thread's 16 bytes of the published bf16 state (SsT[0] =
-    // S^T of this V tile), read before the state is republished and stored
-    // after the step's last prefetch: one coalesced 16-byte store per thread
-    u16x8 hsv = {0, 0, 0, 0, 0, 0, 0, 0};
-    if constexpr (SAVE) {
-      if (tid < 16 * K / 8)
-        hsv = *reinterpret_cast<const u16x8*>(&SsT[0][tid / (K / 8)][8 * (tid % (K / 8))]);
-    }
-    chain_load_a<K>(nxt, ctx, cn);
-    // gate factors of this wave's rows 16w + 4grp + r: e^G, e^(G_last - G),
-    // and e^G_last (row L - 1), from the one G value each lane loaded
-    f32x4 eg, dec;
-    // (two exponentials per lane for its own row, then permuted: the same
-    // values as exponentials of permuted G, with 2 instead of 10 v_exp)
-    const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.G), L - 1));
-    const float egx = __expf(cur.G), decx = __expf(GL - cur.G);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int src = (16 * w + 4 * grp + r) * 4;
-      eg[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(egx)));
-      dec[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(decx)));
-    }
-    const float egl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(egx), L - 1));
-    const u16x8* kf = cur.kf;
-    const u16x8* qf = cur.qf;
-    // stage this chunk's K rows for the K^T operand of the state update
-#pragma unroll
-    for (int b = 0; b < KB; ++b)
-      *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = kf[b];
-
-    // X = K S (hi + lo); the critical path of the step starts here
-    f32x4 xa = zero4(), xb = zero4(), xc = zero4(), xd = zero4();
-#pragma unroll
-    for (int b = 0; b < KB; b += 2) {
-      const u16x8 sh0 = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]);
-      const u16x8 sl0 = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 8 * grp]);
-      const u16x8 sh1 = *reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]);
-      const u16x8 sl1 = *reinterpret_cast<const u16x8*>(&SsT[1][r16][32 * b + 32 + 8 * grp]);
-      xa = mfma16(kf[b], sh0, xa);
-      xb = mfma16(kf[b + 1], sh1, xb);
-      xc = mfma16(kf[b], sl0, xc);
-      xd = mfma16(kf[b + 1], sl1, xd);
-    }
-    {
-      const f32x4 X = (xa + xb) + (xc + xd);
-      f32x4 y;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) y[r] = bf2f(cur.vv[r]) - eg[r] * X[r];
-      u16x4 yh, yl;
-      split_bf4(y, yh, yl);
-      *reinterpret_cast<u16x4*>(&YsT[0][r16][16 * w + 4 * grp]) = yh;
-      *reinterpret_cast<u16x4*>(&YsT[1][r16][16 * w + 4 * grp]) = yl;
-    }
-    __syncthreads();
-    chain_load_b<K>(nxt, ctx, cn);
-    chain_load_q<K>(nxt, ctx, cn);
-
-    // K^T fragments of the update, gathered now (off the critical path):
-    // element ii of lane (r16, grp) is Kl[32b + 8grp + ii][kd0 + r16], two
-    // transposing reads of 4 rows each
-    u16x8 ka[RT][2];
-    const int m4 = r16 >> 2, q4 = r16 & 3;
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-      const int kd0 = w * 16 * RT + 16 * tt + 4 * q4;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const u16x4 lo4 = lds_tr16(&Kl[32 * b + 8 * grp + m4][kd0]);
-        const u16x4 hi4 = lds_tr16(&Kl[32 * b + 8 * grp + 4 + m4][kd0]);
-        ka[tt][b] = u16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-      }
-    }
-    // (Q S_hi)^T = S_hi^T Q^T (needed only for o; S is republished in the
-    // last phase).  The output is formed transposed so that each lane ends
-    // with 4 consecutive columns of one row: one 8-byte store instead of four
-    // 2-byte stores.  The operands are the same fragments, swapped.
-    f32x4 qa = zero4(), qb = zero4();
-#pragma unroll
-    for (int b = 0; b < KB; b += 2) {
-      qa = mfma16(*reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 8 * grp]), qf[b], qa);
-      qb = mfma16(*reinterpret_cast<const u16x8*>(&SsT[0][r16][32 * b + 32 + 8 * grp]),
-                  qf[b + 1], qb);
-    }
-
-    // vnew = Tb Y (three hi/lo terms, independent accumulators)
-    f32x4 vn;
-    u16x4 vbs;   // bf16 vnew (the saved delta)
-    {
-      f32x4 va = zero4(), vb = zero4(), vc = zero4();
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const u16x8 yh = *reinterpret_cast<const u16x8*>(&YsT[0][r16][32 * b + 8 * grp]);
-        const u16x8 yl = *reinterpret_cast<const u16x8*>(&YsT[1][r16][32 * b + 8 * grp]);
-        va = mfma16(cur.tf[b][0], yh, va);
-        vb = mfma16(cur.tf[b][0], yl, vb);
-        vc = mfma16(cur.tf[b][1], yh, vc);
-      }
-      vn = va + (vb + vc);
-    }
-    {
-      u16x4 uh, ul;
-      split_bf4(dec * vn, uh, ul);
-      const u16x4 vb = f2bf4(vn);
-      *reinterpret_cast<u16x4*>(&UsT[0][r16][16 * w + 4 * grp]) = uh;
-      *reinterpret_cast<u16x4*>(&UsT[1][r16][16 * w + 4 * grp]) = ul;
-      vbs = vb;
-      if constexpr (OUT) *reinterpret_cast<u16x4*>(&VnT[r16][16 * w + 4 * grp]) = vb;
-    }
-    __syncthreads();
-    // V and G two chunks ahead, into this step's own buffer (its V and G
-    // were last read in the first phase): they are the first operands a
-    // step waits for, and one step of lead left that wait exposed
-    chain_load_c<K>(cur, ctx, cn2);
-    // saves for the backward, after the step's last prefetch (vector memory
-    // operations retire in issue order: a store ahead of a prefetch would
-    // delay that prefetch's wait): the chunk's start state, transposed
-    // (hs[chunk][head] = S^T, [V][K]), and the chunk's deltas
-    if constexpr (SAVE) {
-      if (tid < 16 * K / 8)
-        *reinterpret_cast<u16x8*>(ws.hs + (((size_t)ci * Hv + h) * V + 16 * vt + tid / (K / 8)) * K +
-                                  8 * (tid % (K / 8))) = hsv;
-      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
-          ws.dl + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        __builtin_amdgcn_raw_buffer_store_b16(
-            vbs[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
-    }
-
-    // S = e^G_L S + K^T U   (U hi + lo)
-    {
-      u16x8 uh[2], ul[2];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        uh[b] = *reinterpret_cast<const u16x8*>(&UsT[0][r16][32 * b + 8 * grp]);
-        ul[b] = *reinterpret_cast<const u16x8*>(&UsT[1][r16][32 * b + 8 * grp]);
-      }
-#pragma unroll
-      for (int tt = 0; tt < RT; ++tt) {
-        f32x4 a0 = Sr[tt] * egl, a1 = zero4();
-        a0 = mfma16(ka[tt][0], uh[0], a0);
-        a1 = mfma16(ka[tt][0], ul[0], a1);
-        a0 = mfma16(ka[tt][1], uh[1], a0);
-        a1 = mfma16(ka[tt][1], ul[1], a1);
-        Sr[tt] = a0 + a1;
-      }
-    }
-    // o^T = scale e^G (Q S)^T + vnew^T P^T: lane holds row 16w + r16,
-    // columns 16 vt + 4 grp .. + 3
-    if constexpr (OUT) {
-      const u16x8 v0 = *reinterpret_cast<const u16x8*>(&VnT[r16][8 * grp]);
-      const u16x8 v1 = *reinterpret_cast<const u16x8*>(&VnT[r16][32 + 8 * grp]);
-      const f32x4 oa = mfma16(v0, cur.pf[0], zero4());
-      const f32x4 ob = mfma16(v1, cur.pf[1], zero4());
-      const f32x4 QS = qa + qb;
-      const float egi = __int_as_float(
-          __builtin_amdgcn_ds_bpermute((16 * w + r16) * 4, __float_as_int(egx)));
-      const u16x4 ov = f2bf4((scale * egi) * QS + (oa + ob));
-      // Buffer store bounded to this chunk's L rows: the hardware drops the
-      // padding rows, so the store needs no branch (a branch here would make
-      // the compiler wait for every outstanding load at the loop head).
-      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-          o + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-      __builtin_amdgcn_raw_buffer_store_b64(
-          __builtin_bit_cast(u32x2, ov), orsrc,
-          (((16 * w + r16) * Hv + h) * V + 16 * vt + 4 * grp) * 2, 0, 0);
-    }
-    publish_state();
-    __syncthreads();
-  };
-
-  // Two operand buffers in ping-pong: a prefetch never has to complete before
-  // the step that does not use it.  The prefetch is unconditional (the last
-  // chunk reloads itself): a conditional load would make the wait-count merge
-  // at the join fall back to waiting for every outstanding load.
-  ChainIn<K> bufA, bufB;
-  if (c_begin < c_end) {
-    chain_load_a<K>(bufA, ctx, c_begin);
-    chain_load_b<K>(bufA, ctx, c_begin);
-    chain_load_q<K>(bufA, ctx, c_begin);
-    chain_load_c<K>(bufA, ctx, c_begin);
-    chain_load_c<K>(bufB, ctx, min(c_begin + 1, c_end - 1));
-  }
-  // Nothing outstanding on entry: the wait counts at the loop head merge the
-  // entry path with the back edge, and the prologue's loads (issued in
-  // another order than the loop's) made that merge wait for nearly every
-  // prefetch at each step start.  The first step needs these loads anyway.
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  // Pairs of steps, then an odd last chunk outside the loop: an exit between
-  // the two steps of a pair would be a path back to the loop head after one
-  // step, and the wait counts there would have to cover it (a wait for
-  // nearly every outstanding prefetch at each pair's start).
-  int ci = c_begin;
-  for (; ci + 1 < c_end; ci += 2) {
-    step(bufA, bufB, ci, ci + 1, min(ci + 2, c_end - 1));
-    step(bufB, bufA, ci + 1, min(ci + 2, c_end - 1), min(ci + 3, c_end - 1));
-  }
-  if (ci < c_end) step(bufA, bufB, ci, ci, ci);
-
-  if (ht) {
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
-        ht[tile + (size_t)kd * V] = Sr[tt][r];
-      }
-    }
-  }
-}
-
 // ------------------------------------------------------------- host ----
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -833,13 +443,8 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
     hipLaunchKernelGGL((chunk_prep_kernel<K, BWD>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0,
                        st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised
-  if constexpr (OUT && !BWD)
-    launch_chain_sw<K>(l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V,
-                       scale, ws, st);
-  else
-    hipLaunchKernelGGL((chunk_chain_kernel<K, BWD, OUT>), dim3(N * Hv * (V / 16)), dim3(256), 0,
-                       st, l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
-                       OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  launch_chain_sw<K, BWD, OUT>(l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
+                               OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws, st);
 }
 
 void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,

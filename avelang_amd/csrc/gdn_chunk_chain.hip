@@ -1,6 +1,6 @@
 // Forward chain of the chunked prefill, state-wave form (gfx950).
 //
-// One workgroup of two waves per (sequence, v-head, 16-column V tile),
+// One workgroup of three waves per (sequence, v-head, 16-column V tile),
 // sequential over the sequence's chunks of 64 tokens:
 //
 //   wave 0, the state wave, holds every key row of the tile's fp32 state in
@@ -10,16 +10,18 @@
 //   (Tb = (I + A)^-1 diag(beta) from the prep kernel; K S, Tb Y and K^T U
 //   as hi + lo bf16 MFMA products).  Each product's result tile is the next
 //   product's B operand where it stands (row orders below), so no LDS
-//   exchange and no barrier sits inside the step.
+//   exchange sits inside the step, and every operand comes from LDS.
 //
-//   wave 1, the stage wave, fills LDS with chunk c+1's operands (the K rows,
-//   the Tb fragments, the V tile as fp32 in the state wave's layout, e^G
-//   and e^(G_last - G))
-//   and forms chunk c-1's output from the state and vnew fragments the state
-//   wave leaves in LDS:  o = scale e^G (Q S) + P vnew.
+//   wave 1, the stage wave, loads chunk c+2's K rows and Tb fragments
+//   straight into LDS (buffer_load ... lds) while step c runs.
 //
-// One s_barrier per chunk step hands the buffers over (two stage buffers,
-// two output buffers).  The state wave issues no global load at all.
+//   wave 2, the output wave, writes chunk c+1's V tile (as fp32, in the
+//   state wave's layout) and gate factors into LDS and forms chunk c-1's
+//   output from the state and vnew fragments the state wave leaves in LDS:
+//       o = scale e^G (Q S) + P vnew.
+//
+// One s_barrier per chunk step hands the buffers over (three stage buffers,
+// three output buffers).  The state wave issues no global load at all.
 //
 // Row orders.  An MFMA result tile puts rows 4 grp + r (r < 4) in lane
 // (n, grp); a B operand of k-block b takes reduction slots 8 grp + i (i < 8)
@@ -39,6 +41,8 @@ namespace gdn {
 __device__ __forceinline__ int rho_row(int T, int m) {
   return 32 * (T >> 1) + 8 * (m >> 2) + 4 * (T & 1) + (m & 3);
 }
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ u16x8 cat8(u16x4 a, u16x4 b) {
   return u16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
@@ -69,7 +73,11 @@ struct KLayout {
   __device__ static constexpr int row(int r) { return r * RS + (r >> 4) * GP; }
 };
 
-template <int K>
+// SAVE: store the state at every chunk start (ws.hs, bf16, transposed) and
+// the per-token delta vnew (ws.dl, bf16) for the backward.  OUT: write o and
+// ht.  Forward <K, false, true>, the backward's recomputation <K, true,
+// false>, a training forward <K, true, true>.
+template <int K, bool SAVE, bool OUT>
 __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
@@ -353,9 +361,10 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
     // steps before it is used (two sets, the loop unrolled by two), and
     // every step issues the same loads and stores, so each wait names an
     // exact count.
-    constexpr int kQP = 4 * KB + 6;      // Q / P loads per chunk
-    constexpr int kVG = 3;               // V tile (2) + G (1)
-    constexpr int kStep = 4 + kQP + kVG; // output stores + loads per step
+    constexpr int kQP = OUT ? 4 * KB + 6 : 0;   // Q / P loads per chunk
+    constexpr int kVG = 3;                      // V tile (2) + G (1)
+    constexpr int kSave = SAVE ? KB + 16 : 0;   // state and delta stores per chunk
+    constexpr int kStep = (OUT ? 4 : 0) + kSave + kQP + kVG;   // stores + loads per step
     const int rowq = Hqk * K * 2;
     struct Regs {
       u16x8 qf[4][KB];   // Q rows 16 ti + r16, B operand of (Q S)^T
@@ -365,6 +374,7 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
     };
     Regs rA, rB;
     auto load_qp = [&](Regs& r, int j) {
+      if constexpr (!OUT) return;
       const int ci = c_begin + j;
       const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
       const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
@@ -422,14 +432,14 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
     };
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     // o^T tiles of chunk j: lane (r16, grp) holds token row 16 ti + r16,
-    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile).  With
-    // live = false (no chunk yet) the four stores go to an empty resource
-    // and are dropped.
+    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile); SAVE: the
+    // chunk's start state (hs[chunk][v-head] = S^T, [V][K]: the state
+    // fragments as they stand, 16 bytes per k-block) and its deltas (dl,
+    // token-major).  With live = false (no chunk yet) every store goes to an
+    // empty resource and is dropped.
     auto output = [&](const Regs& r, int j, bool live) {
       const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
       const int b3 = j % 3;
-      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-          o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
       u16x8 sh[KB], vx[2];
       if (live) {
 #pragma unroll
@@ -437,6 +447,27 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
         vx[0] = Vx[b3][0][lane];
         vx[1] = Vx[b3][1][lane];
       }
+      if constexpr (SAVE) {
+        const size_t ci = live ? (size_t)(c_begin + j) : 0;
+        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+            ws.hs + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sh[b]), hr,
+                                                 ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
+        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+            ws.dl + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_raw_buffer_store_b16(
+                vx[b][i], dr, (((32 * b + 8 * grp + i) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
+        }
+      }
+      if constexpr (!OUT) return;
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
         u16x4 ov = {0, 0, 0, 0};
@@ -489,19 +520,37 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
   }
 }
 
-template <int K>
+template <int K, bool SAVE, bool OUT>
 void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
                      float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
                      int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st) {
-  hipLaunchKernelGGL((chunk_chain_sw_kernel<K>), dim3(N * Hv * (V / 16)), dim3(192), 0, st, q,
-                     k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT>), dim3(N * Hv * (V / 16)), dim3(192), 0,
+                     st, q, k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
 }
 
-template void launch_chain_sw<64>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                  const float*, float*, uint16_t*, const int32_t*, int, int, int,
-                                  int, int, int, float, const ChunkWs&, hipStream_t);
-template void launch_chain_sw<128>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                   const float*, float*, uint16_t*, const int32_t*, int, int,
-                                   int, int, int, int, float, const ChunkWs&, hipStream_t);
+template void launch_chain_sw<64, false, true>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                                 const float*, float*, uint16_t*, const int32_t*, int,
+                                                 int, int, int, int, int, float, const ChunkWs&,
+                                                 hipStream_t);
+template void launch_chain_sw<64, true, false>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                                 const float*, float*, uint16_t*, const int32_t*, int,
+                                                 int, int, int, int, int, float, const ChunkWs&,
+                                                 hipStream_t);
+template void launch_chain_sw<64, true, true>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                                 const float*, float*, uint16_t*, const int32_t*, int,
+                                                 int, int, int, int, int, float, const ChunkWs&,
+                                                 hipStream_t);
+template void launch_chain_sw<128, false, true>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                                 const float*, float*, uint16_t*, const int32_t*, int,
+                                                 int, int, int, int, int, float, const ChunkWs&,
+                                                 hipStream_t);
+template void launch_chain_sw<128, true, false>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                                 const float*, float*, uint16_t*, const int32_t*, int,
+                                                 int, int, int, int, int, float, const ChunkWs&,
+                                                 hipStream_t);
+template void launch_chain_sw<128, true, true>(const uint16_t*, const uint16_t*, const uint16_t*,
+                                                 const float*, float*, uint16_t*, const int32_t*, int,
+                                                 int, int, int, int, int, float, const ChunkWs&,
+                                                 hipStream_t);
 
 }  // namespace gdn
