@@ -25,6 +25,7 @@ EXPORTS = (
     "gdn_recurrent_fwd",
     "gdn_last_error",
     "gdn_abi_version",
+    "gdn_cu_seqlens_check",
     # include/gdn_layer.h
     "gdn_gating_fwd",
     "gdn_l2norm_fwd",
@@ -109,6 +110,8 @@ def lib():
         h.gdn_last_error.argtypes = []
         h.gdn_abi_version.restype = _i
         h.gdn_abi_version.argtypes = []
+        h.gdn_cu_seqlens_check.restype = _i
+        h.gdn_cu_seqlens_check.argtypes = [_vp, _i, _i]
         h.gdn_gating_fwd.restype = _i
         h.gdn_gating_fwd.argtypes = [
             _vp, _vp, _vp, _vp, _vp, _vp,     # A_log a b dt_bias g beta

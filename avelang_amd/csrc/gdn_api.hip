@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <string>
 
+#include "gdn_chunk.h"
 #include "gdn_common.h"
 
 namespace gdn_host {
@@ -77,3 +78,15 @@ int validate_common(const void* q, const void* k, const void* v, const float* g,
 extern "C" const char* gdn_last_error(void) { return gdn_host::g_last_error.c_str(); }
 
 extern "C" int gdn_abi_version(void) { return 101; }
+
+// Host-side form of the device check the chunked kernels make (declared in
+// gdn.h): the contract on cu_seqlens.
+extern "C" int gdn_cu_seqlens_check(const int32_t* cu_seqlens, int N, int total_tokens) {
+  if (!cu_seqlens) return gdn_host::fail(GDN_ERR_NULL, "gdn_cu_seqlens_check: cu_seqlens is NULL");
+  if (N < 0 || total_tokens < 0)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_cu_seqlens_check: N and total_tokens must be >= 0");
+  static const char* what[] = {"", "cu_seqlens[0] must be 0", "cu_seqlens must be non-decreasing",
+                               "cu_seqlens[N] must equal the packed token count"};
+  const int v = gdn::cu_seqlens_violation(cu_seqlens, N, total_tokens);
+  return v ? gdn_host::fail(GDN_ERR_SEQLENS, std::string("gdn_cu_seqlens_check: ") + what[v]) : GDN_OK;
+}

@@ -12,6 +12,7 @@ namespace gdn {
 // stated.  The backward-only buffers are NULL in a plain forward call.
 struct ChunkWs {
   int32_t* off;     // [N+1] first global chunk of each sequence
+  int32_t* status;  // [1] 0, or the cu_seqlens violation the chunk table found
   float* gate;      // [NC][Hv][64]: G_i, the chunk-local cumulative log-decay
   u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
   u16x8* pfrag;     // [NC][Hv][4][2][64]
@@ -35,6 +36,27 @@ __device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int 
     e = s + T;
   }
 }
+
+// The contract on cu_seqlens [N+1]: cu[0] == 0, cu[n] <= cu[n+1], cu[N] ==
+// total.  Returns 0, or the first violation found: 1 cu[0] != 0, 2 a
+// decrease, 3 cu[N] != total.  The chunk table kernel checks the same three
+// conditions on the device.
+__host__ __device__ inline int cu_seqlens_violation(const int32_t* cu, int N, int total) {
+  if (cu[0] != 0) return 1;
+  for (int n = 0; n < N; ++n)
+    if (cu[n + 1] < cu[n]) return 2;
+  return cu[N] != total ? 3 : 0;
+}
+
+// Buffers zero-filled when the chunk table found a cu_seqlens violation.
+struct ZeroList {
+  void* p[5];
+  size_t bytes[5];
+};
+
+// Enqueue the zero-fill of `z` conditional on *status != 0 (one small launch;
+// its workgroups return at once when the status is 0).
+void launch_zero_on_violation(const int32_t* status, const ZeroList& z, hipStream_t st);
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
@@ -62,7 +84,7 @@ __device__ __forceinline__ u16x8 lds_colfrag(const uint16_t* X, int ld, int k0, 
 
 // Workspace plan (byte offsets into the caller's buffer).
 struct WsPlan {
-  size_t off, gate, tfrag, pfrag, qn, kn, total;
+  size_t off, status, gate, tfrag, pfrag, qn, kn, total;
   // backward only (0 when not planned)
   size_t tmat, ttfrag, ptfrag, hs, dl, dse, dd;
   long long ncmax;

@@ -35,13 +35,31 @@
 namespace gdn {
 
 // -------------------------------------------------------- chunk table ----
+// Sequence -> first-chunk offsets, after checking the cu_seqlens contract
+// (cu[0] == 0, non-decreasing, cu[N] == total).  A violation is recorded in
+// *status and every sequence is then treated as empty (all offsets 0), so
+// that no later kernel reads or writes past the packed tokens; the caller's
+// outputs are zero-filled by zero_on_violation_kernel.
 __global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restrict__ cu,
                                                           int N, int T, int total,
-                                                          int ncmax, int32_t* __restrict__ off) {
+                                                          int ncmax, int32_t* __restrict__ off,
+                                                          int32_t* __restrict__ status) {
   __shared__ int part[257];
+  __shared__ int bad;
   const int tid = threadIdx.x;
   const int per = (N + 255) / 256;
   const int a = min(tid * per, N), b = min(a + per, N);
+  if (tid == 0) bad = cu[0] != 0 ? 1 : (cu[N] != total ? 3 : 0);
+  __syncthreads();
+  for (int n = a; n < b; ++n)
+    if (cu[n + 1] < cu[n]) atomicMax(&bad, 2);
+  __syncthreads();
+  if (bad) {
+    for (int n = tid; n <= N; n += 256) off[n] = 0;
+    if (tid == 0) *status = bad;
+    return;
+  }
+  if (tid == 0) *status = 0;
   int sum = 0;
   for (int n = a; n < b; ++n) {
     int s, e;
@@ -63,6 +81,30 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(const int32_t* __restr
     run += (e - s + kChunk - 1) / kChunk;
   }
   if (tid == 255) off[N] = min(part[256], ncmax);
+}
+
+__global__ __launch_bounds__(256) void zero_on_violation_kernel(const int32_t* __restrict__ status,
+                                                                ZeroList z) {
+  if (*status == 0) return;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (int i = 0; i < 5; ++i) {
+    // 16-byte stores over the 16-byte-aligned body, then the tail bytes
+    unsigned char* p = static_cast<unsigned char*>(z.p[i]);
+    if (!p) continue;
+    const size_t n = z.bytes[i];
+    const size_t head = (16 - ((uintptr_t)p & 15)) & 15;
+    const size_t h = head < n ? head : n;
+    const size_t body = (n - h) / 16;
+    for (size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x; j < body; j += stride)
+      reinterpret_cast<uint4*>(p + h)[j] = uint4{0, 0, 0, 0};
+    for (size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x; j < h + (n - h - 16 * body);
+         j += stride)
+      p[j < h ? j : h + 16 * body + (j - h)] = 0;
+  }
+}
+
+void launch_zero_on_violation(const int32_t* status, const ZeroList& z, hipStream_t st) {
+  hipLaunchKernelGGL(zero_on_violation_kernel, dim3(256), dim3(256), 0, st, status, z);
 }
 
 // ---------------------------------------------------------- prep (K1) ----
@@ -389,6 +431,7 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
     return here;
   };
   p.off = take((size_t)(N + 1) * 4);
+  p.status = take(4);
   p.gate = take(nch * 64 * 4);
   p.tfrag = take(nch * 4 * 2 * 2 * 64 * 16);
   p.pfrag = take(nch * 4 * 2 * 64 * 16);
@@ -413,6 +456,7 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
 ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb) {
   ChunkWs ws{};
   ws.off = reinterpret_cast<int32_t*>(wsb + p.off);
+  ws.status = reinterpret_cast<int32_t*>(wsb + p.status);
   ws.gate = reinterpret_cast<float*>(wsb + p.gate);
   ws.tfrag = reinterpret_cast<u16x8*>(wsb + p.tfrag);
   ws.pfrag = reinterpret_cast<u16x8*>(wsb + p.pfrag);
@@ -438,13 +482,21 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
   const int total = B * T;
   if (cu)
     hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, st, cu, N, T, total,
-                       (int)p.ncmax, ws.off);
+                       (int)p.ncmax, ws.off, ws.status);
   if (p.ncmax > 0)
     hipLaunchKernelGGL((chunk_prep_kernel<K, BWD>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0,
                        st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised
   launch_chain_sw<K, BWD, OUT>(l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
                                OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws, st);
+  // a cu_seqlens violation left every sequence empty: o is zero-filled (and
+  // ht = h0, written by the chain for an empty sequence)
+  if (cu && OUT) {
+    ZeroList z{};
+    z.p[0] = o;
+    z.bytes[0] = (size_t)total * Hv * V * 2;
+    launch_zero_on_violation(ws.status, z, st);
+  }
 }
 
 void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,

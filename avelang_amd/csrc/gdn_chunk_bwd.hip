@@ -1117,5 +1117,20 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   else if (V == 128) GDN_BWD(64, 128);
   else GDN_BWD(64, 64);
 #undef GDN_BWD
+  if (cu_seqlens) {
+    // a cu_seqlens violation (found by the forward's chunk table, in this
+    // workspace) left every sequence empty: the gradients are zero-filled
+    // (and dh0 = dht, written by the reverse chain for an empty sequence)
+    gdn::ZeroList z{};
+    const size_t nqk = (size_t)tokens * Hqk * K * 2, nv = (size_t)tokens * Hv * V * 2;
+    const size_t ng = (size_t)tokens * Hv * 4;
+    void* outs[] = {dq, dk, dv, dg, dbeta};
+    const size_t sizes[] = {nqk, nqk, nv, ng, ng};
+    for (int i = 0; i < 5; ++i) {
+      z.p[i] = outs[i];
+      z.bytes[i] = sizes[i];
+    }
+    gdn::launch_zero_on_violation(gdn::ws_pointers(p, wsb).status, z, st);
+  }
   return gdn_host::check_launch("gdn_chunk_bwd");
 }

@@ -88,9 +88,13 @@ def _check_inputs(q, k, v, g, beta, initial_state, cu_seqlens, name):
     if cu_seqlens is not None:
         N = cu_seqlens.numel() - 1
         if cu_seqlens.device.type == "cpu":
-            c = cu_seqlens.tolist()
-            if c[0] != 0 or c[-1] != T or any(b < a for a, b in zip(c[:-1], c[1:])):
-                raise ValueError(f"{name}: cu_seqlens must rise monotonically from 0 to T={T}.")
+            # the library's own check of the contract (the chunked kernels
+            # repeat it on the device, where a violation empties every
+            # sequence instead of raising)
+            c32 = cu_seqlens.to(torch.int32).contiguous()
+            lib = _native.lib()
+            if lib.gdn_cu_seqlens_check(c32.data_ptr(), N, T) != 0:
+                raise ValueError(f"{name}: {lib.gdn_last_error().decode()} (T={T}).")
         elif cu_seqlens.device != dev:
             raise ValueError(f"{name}: cu_seqlens must be on {dev} or the CPU.")
         cu = cu_seqlens.to(device=dev, dtype=torch.int32, non_blocking=True).contiguous()

@@ -24,7 +24,14 @@
  *     v-head h reads qk-head h / (Hv / Hqk).
  *   - cu_seqlens (nullable) is an int32 device array [N+1] of packed
  *     sequence offsets; it requires B == 1.  Without it N == B and every
- *     batch row is one sequence of length T.
+ *     batch row is one sequence of length T.  Contract: cu_seqlens[0] == 0,
+ *     non-decreasing, cu_seqlens[N] == T.  Being device memory it is not
+ *     read on the host; gdn_cu_seqlens_check() makes the same check on a
+ *     host copy.  The chunked entry points (gdn_chunk_fwd, _fwd_save,
+ *     _bwd) also check it on the device: on a violation every sequence is
+ *     treated as empty -- o and the gradients are zero-filled, ht = h0 and
+ *     dh0 = dht -- and the call still returns 0.  The recurrent entry points
+ *     clamp each sequence's range to [0, T] instead.
  *   - Return value: 0 = success; < 0 = argument error (nothing enqueued);
  *     > 0 = a hipError_t from a launch.  gdn_last_error() gives a
  *     thread-local message for the last failing call of this thread.
@@ -150,6 +157,16 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v,
 /* Bytes of device workspace gdn_chunk_bwd (and gdn_chunk_fwd_save) need. */
 size_t gdn_chunk_bwd_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
                                      int N, int has_cu_seqlens, int use_qk_l2norm);
+
+/*
+ * Host-side check of the cu_seqlens contract above on a host array [N+1]:
+ * GDN_OK, or GDN_ERR_SEQLENS naming the first violation (gdn_last_error()).
+ * The same conditions the chunked kernels check on the device.  No
+ * counterpart in the reference (it has no varlen plumbing); callers that
+ * hold cu_seqlens on the host use it to get an error instead of the
+ * device-side empty-sequence fallback.
+ */
+int gdn_cu_seqlens_check(const int32_t* cu_seqlens, int N, int total_tokens);
 
 /* Thread-local message describing the last failure (never NULL). */
 const char* gdn_last_error(void);

@@ -29,7 +29,8 @@ def test_header_declares_expected_entry_points():
     assert _declared(("gdn.h",)) == ["gdn_abi_version", "gdn_chunk_bwd",
                                      "gdn_chunk_bwd_workspace_bytes", "gdn_chunk_fwd",
                                      "gdn_chunk_fwd_save", "gdn_chunk_workspace_bytes",
-                                     "gdn_last_error", "gdn_recurrent_fwd"]
+                                     "gdn_cu_seqlens_check", "gdn_last_error",
+                                     "gdn_recurrent_fwd"]
     assert _declared(("gdn_layer.h",)) == [
         "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_gating_fwd",
         "gdn_l2norm_fwd", "gdn_recurrent_fwd_indexed", "gdn_recurrent_fwd_spec",
@@ -266,3 +267,28 @@ def test_layer_empty_problems_launch_nothing(lib):
     assert _convu(lib, B=0) == 0
     assert _reci(lib, N=0, B=0) == 0
     assert _recs(lib, N=0, B=0) == 0
+
+
+@pytest.mark.parametrize("cu, total, msg", [
+    ([0, 3, 3, 10], 10, None),
+    ([0], 0, None),                                  # N = 0
+    ([0, 0, 0], 0, None),                            # empty sequences only
+    ([1, 3, 10], 10, "cu_seqlens[0] must be 0"),
+    ([0, 5, 4, 10], 10, "non-decreasing"),
+    ([0, 3, 9], 10, "must equal the packed token count"),
+    ([0, 3, 11], 10, "must equal the packed token count"),
+])
+def test_cu_seqlens_contract_host_check(lib, cu, total, msg):
+    """gdn_cu_seqlens_check: the contract the chunked kernels check on the device."""
+    arr = (ctypes.c_int32 * len(cu))(*cu)
+    rc = lib.gdn_cu_seqlens_check(arr, len(cu) - 1, total)
+    if msg is None:
+        assert rc == 0
+    else:
+        assert rc == -3 and msg in lib.gdn_last_error().decode()
+
+
+def test_cu_seqlens_check_arguments(lib):
+    assert lib.gdn_cu_seqlens_check(None, 1, 4) == -1
+    arr = (ctypes.c_int32 * 2)(0, 4)
+    assert lib.gdn_cu_seqlens_check(arr, -1, 4) == -2

@@ -107,7 +107,7 @@ def test_bwd_cfg0_shape(rocm_device):
     _case(rocm_device, 1, 256, 4, 4, 64, 64, seed=3, h0_scale=0.0, dht_scale=0.0, what="cfg0")
 
 
-@pytest.mark.parametrize("K,V", [(64, 128), (128, 64)])
+@pytest.mark.parametrize("K,V", [(64, 64), (64, 128), (128, 64)])
 def test_bwd_head_sizes(rocm_device, K, V):
     _case(rocm_device, 1, 130, 2, 4, K, V, seed=K + V, what=f"K{K} V{V}")
 
