@@ -26,6 +26,7 @@ EXPORTS = (
     "gdn_last_error",
     "gdn_abi_version",
     "gdn_cu_seqlens_check",
+    "gdn_chunk_fwd_noalloc",
     # include/gdn_layer.h
     "gdn_gating_fwd",
     "gdn_l2norm_fwd",
@@ -110,6 +111,8 @@ def lib():
         h.gdn_last_error.argtypes = []
         h.gdn_abi_version.restype = _i
         h.gdn_abi_version.argtypes = []
+        h.gdn_chunk_fwd_noalloc.restype = _i
+        h.gdn_chunk_fwd_noalloc.argtypes = h.gdn_recurrent_fwd.argtypes
         h.gdn_cu_seqlens_check.restype = _i
         h.gdn_cu_seqlens_check.argtypes = [_vp, _i, _i]
         h.gdn_gating_fwd.restype = _i

@@ -30,6 +30,8 @@
 // Precision: the three products that feed the state (K S, Tb Y, K^T U) use
 // hi+lo bf16 splits of their fp32 operand(s); Q S and P vnew (output only)
 // use single bf16.
+#include <mutex>
+
 #include "gdn_chunk.h"
 
 namespace gdn {
@@ -558,6 +560,74 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
                         static_cast<unsigned char*>(workspace),
                         static_cast<hipStream_t>(stream));
   return gdn_host::check_launch("gdn_chunk_fwd");
+}
+
+// ----------------------------------------------- allocation-free form ----
+// Device scratch of gdn_chunk_fwd_noalloc: one array per GPU the library runs
+// on, held until the process ends.  Its name is a host-side stand-in: host
+// code uses the per-device address from hipGetSymbolAddress, never the name.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 256;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];   // address of `scratch` on each device, once looked up
+
+// Address of the current device's scratch (looked up once per device).
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return gdn_host::fail(static_cast<int>(e), std::string("gdn_chunk_fwd_noalloc: hipGetDevice: ") +
+                                                   hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_fwd_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return gdn_host::fail(e != hipSuccess ? static_cast<int>(e) : GDN_ERR_NULL,
+                            std::string("gdn_chunk_fwd_noalloc: hipGetSymbolAddress: ") +
+                                hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GDN_OK;
+}
+}  // namespace
+
+// gdn_chunk_fwd with the library's own scratch in place of a workspace
+// (declared in gdn.h): no allocation of any kind.
+extern "C" int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const float* g,
+                                     const float* beta, const float* h0, float* ht, void* o,
+                                     const int32_t* cu_seqlens, int B, int T, int Hqk, int Hv,
+                                     int K, int V, int N, float scale, int use_qk_l2norm,
+                                     void* stream) {
+  int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk, Hv,
+                                     K, V, N);
+  if (rc) return rc;
+  if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
+  const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
+                                     use_qk_l2norm != 0, false);
+  if (p.total > kNoAllocScratchBytes)
+    return gdn_host::fail(GDN_ERR_WORKSPACE,
+                          "gdn_chunk_fwd_noalloc: the problem needs " + std::to_string(p.total) +
+                              " bytes of scratch, more than the library's " +
+                              std::to_string(kNoAllocScratchBytes) +
+                              " (use gdn_chunk_fwd with a workspace)");
+  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_fwd_noalloc: problem too large");
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  gdn::launch_chunk_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                        static_cast<const uint16_t*>(v), g, beta, h0, ht,
+                        static_cast<uint16_t*>(o), cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
+                        use_qk_l2norm != 0, gdn::FwdMode::kForward, p,
+                        static_cast<unsigned char*>(ws), static_cast<hipStream_t>(stream));
+  return gdn_host::check_launch("gdn_chunk_fwd_noalloc");
 }
 
 extern "C" int gdn_chunk_fwd_save(const void* q, const void* k, const void* v, const float* g,

@@ -83,6 +83,27 @@ size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
                                  int N, int has_cu_seqlens, int use_qk_l2norm);
 
 /*
+ * gdn_chunk_fwd without a workspace argument: the library's own device
+ * scratch (a fixed array of 32 MiB per GPU, held until the process ends)
+ * takes its place, so the call allocates nothing -- no hipMalloc, no
+ * hipFree, no allocating library routine.  No counterpart in the
+ * reference; it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).
+ * Problems whose gdn_chunk_workspace_bytes(...) exceeds 32 MiB (about 1300
+ * chunk x v-head pairs, e.g. T = 2048 at 32 v-heads) are rejected with
+ * GDN_ERR_WORKSPACE before anything is enqueued.  Every call on one GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (different
+ * streams, or host threads) race and must be serialised by the caller.
+ */
+int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v,
+                          const float* g, const float* beta,
+                          const float* h0, float* ht, void* o,
+                          const int32_t* cu_seqlens,
+                          int B, int T, int Hqk, int Hv, int K, int V, int N,
+                          float scale, int use_qk_l2norm,
+                          void* stream);
+
+/*
  * Training forward: gdn_chunk_fwd's results (o, ht) plus, in `workspace`
  * (at least gdn_chunk_bwd_workspace_bytes(...)), everything gdn_chunk_bwd
  * needs, so that a later gdn_chunk_bwd(..., saved = 1, same workspace) on

@@ -28,9 +28,9 @@ def _declared(headers=("gdn.h", "gdn_layer.h")):
 def test_header_declares_expected_entry_points():
     assert _declared(("gdn.h",)) == ["gdn_abi_version", "gdn_chunk_bwd",
                                      "gdn_chunk_bwd_workspace_bytes", "gdn_chunk_fwd",
-                                     "gdn_chunk_fwd_save", "gdn_chunk_workspace_bytes",
-                                     "gdn_cu_seqlens_check", "gdn_last_error",
-                                     "gdn_recurrent_fwd"]
+                                     "gdn_chunk_fwd_noalloc", "gdn_chunk_fwd_save",
+                                     "gdn_chunk_workspace_bytes", "gdn_cu_seqlens_check",
+                                     "gdn_last_error", "gdn_recurrent_fwd"]
     assert _declared(("gdn_layer.h",)) == [
         "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_gating_fwd",
         "gdn_l2norm_fwd", "gdn_recurrent_fwd_indexed", "gdn_recurrent_fwd_spec",
@@ -292,3 +292,13 @@ def test_cu_seqlens_check_arguments(lib):
     assert lib.gdn_cu_seqlens_check(None, 1, 4) == -1
     arr = (ctypes.c_int32 * 2)(0, 4)
     assert lib.gdn_cu_seqlens_check(arr, -1, 4) == -2
+
+
+def test_noalloc_scratch_limit_checked_before_launch(lib):
+    """gdn_chunk_fwd_noalloc rejects a problem over its 32 MiB scratch first."""
+    need = lib.gdn_chunk_workspace_bytes(1, 8192, 16, 32, 128, 128, 1, 0, 0)
+    assert need > (32 << 20)
+    fake = [1 << 28, 2 << 28, 3 << 28, 4 << 28, 5 << 28, None, None, 6 << 28, None]
+    assert lib.gdn_chunk_fwd_noalloc(*fake, 1, 8192, 16, 32, 128, 128, 1, 0.1, 0, None) == -4
+    assert "scratch" in lib.gdn_last_error().decode()
+    assert lib.gdn_chunk_fwd_noalloc(None, *fake[1:], 1, 64, 2, 4, 128, 128, 1, 0.1, 0, None) == -1
