@@ -18,8 +18,10 @@ from .gated_delta_rule import (  # noqa: F401
     chunk_gated_delta_rule,
     chunk_gated_delta_rule_bwd,
     chunk_gated_delta_rule_fwd_save,
+    chunk_gated_delta_rule_gated,
     chunk_workspace_bytes,
     fused_recurrent_gated_delta_rule,
+    fused_recurrent_gated_delta_rule_gated,
 )
 from .layer_ops import (  # noqa: F401
     causal_conv1d_fn,
@@ -34,6 +36,8 @@ __all__ = [
     "chunk_gated_delta_rule_bwd",
     "chunk_gated_delta_rule_fwd_save",
     "fused_recurrent_gated_delta_rule",
+    "chunk_gated_delta_rule_gated",
+    "fused_recurrent_gated_delta_rule_gated",
     "chunk_workspace_bytes",
     "chunk_bwd_workspace_bytes",
     "fused_gdn_gating",

@@ -27,6 +27,8 @@ EXPORTS = (
     "gdn_abi_version",
     "gdn_cu_seqlens_check",
     "gdn_chunk_fwd_noalloc",
+    "gdn_chunk_fwd_gating",
+    "gdn_recurrent_fwd_gating",
     # include/gdn_layer.h
     "gdn_gating_fwd",
     "gdn_l2norm_fwd",
@@ -113,6 +115,13 @@ def lib():
         h.gdn_abi_version.argtypes = []
         h.gdn_chunk_fwd_noalloc.restype = _i
         h.gdn_chunk_fwd_noalloc.argtypes = h.gdn_recurrent_fwd.argtypes
+        _gate = [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _f]   # A_log, a, b, dt_bias, dtypes, softplus
+        h.gdn_chunk_fwd_gating.restype = _i
+        h.gdn_chunk_fwd_gating.argtypes = ([_vp] * 3 + _gate + [_vp] * 4 + [_i] * 7
+                                           + [_f, _i, _vp, _sz, _vp])
+        h.gdn_recurrent_fwd_gating.restype = _i
+        h.gdn_recurrent_fwd_gating.argtypes = ([_vp] * 3 + _gate + [_vp] * 5 + [_i] * 8
+                                               + [_f, _i, _vp])
         h.gdn_cu_seqlens_check.restype = _i
         h.gdn_cu_seqlens_check.argtypes = [_vp, _i, _i]
         h.gdn_gating_fwd.restype = _i

@@ -73,6 +73,25 @@ int validate_common(const void* q, const void* k, const void* v, const float* g,
   return GDN_OK;
 }
 
+// Arguments of the gating the fused entry points compute inside (a and b
+// are null-checked by validate_common in place of g and beta).
+int validate_gate(const char* name, const void* A_log, const void* dt_bias, int a_dtype,
+                  int b_dtype, int p_dtype, float sp_beta, long long tokens) {
+  if (!gdn::dtype_ok(a_dtype) || !gdn::dtype_ok(b_dtype) || !gdn::dtype_ok(p_dtype))
+    return fail(GDN_ERR_SHAPE, std::string(name) + ": unsupported dtype code");
+  if (!(sp_beta > 0.f)) return fail(GDN_ERR_SHAPE, std::string(name) + ": softplus beta must be > 0");
+  if (tokens > 0 && (!A_log || !dt_bias))
+    return fail(GDN_ERR_NULL, std::string(name) + ": A_log and dt_bias must be non-NULL");
+  return GDN_OK;
+}
+
+// The fused kernels address a, b with 32-bit byte offsets (4 bytes per element).
+int validate_gate_size(const char* name, long long elements) {
+  if (elements * 4 >= (1LL << 31))
+    return fail(GDN_ERR_SHAPE, std::string(name) + ": a, b too large for the fused gating");
+  return GDN_OK;
+}
+
 }  // namespace gdn_host
 
 extern "C" const char* gdn_last_error(void) { return gdn_host::g_last_error.c_str(); }

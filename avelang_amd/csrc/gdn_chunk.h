@@ -103,7 +103,7 @@ void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
                       const float* beta, const float* h0, float* ht, uint16_t* o,
                       const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N,
                       float scale, bool l2, FwdMode mode, const WsPlan& p, unsigned char* wsb,
-                      hipStream_t st);
+                      hipStream_t st, const GateIn& gate = GateIn{});
 
 ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb);
 

@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ g, const float* __restrict__ beta,
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, float scale,
-    int l2norm, ChunkWs ws) {
+    int l2norm, ChunkWs ws, GateIn gate) {
   constexpr int KB = K / 32;
   // strictly lower 16 x 16 blocks of A only (block (bi, m), m < bi, at
   // bi (bi - 1) / 2 + m; row stride 20 keeps float4 rows aligned and the 16
@@ -182,8 +182,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   float gv = 0.f, bv = 0.f;
   if (w == 0) {
     const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
-    gv = g[grow];
-    bv = beta[grow];
+    // gating computed here (gate.a set) or read from g / beta
+    if (gate.a) {
+      gate_at(gate, (long long)grow, h, gv, bv);
+    } else {
+      gv = g[grow];
+      bv = beta[grow];
+    }
   }
   // K / Q rows straight into MFMA fragments (this wave's rows); the K rows
   // are also staged in LDS, where the other waves read them as B operands.
@@ -479,7 +484,7 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
                          const float* g, const float* beta, const float* h0, float* ht,
                          uint16_t* o, const int32_t* cu, int B, int T, int Hqk, int Hv, int V,
                          int N, float scale, bool l2, const WsPlan& p, unsigned char* wsb,
-                         hipStream_t st) {
+                         hipStream_t st, const GateIn& gate) {
   const ChunkWs ws = ws_pointers(p, wsb);
   const int total = B * T;
   if (cu)
@@ -487,7 +492,7 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
                        (int)p.ncmax, ws.off, ws.status);
   if (p.ncmax > 0)
     hipLaunchKernelGGL((chunk_prep_kernel<K, BWD>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0,
-                       st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws);
+                       st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws, gate);
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised
   launch_chain_sw<K, BWD, OUT>(l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
                                OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws, st);
@@ -505,10 +510,10 @@ void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
                       const float* beta, const float* h0, float* ht, uint16_t* o,
                       const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N,
                       float scale, bool l2, FwdMode mode, const WsPlan& p, unsigned char* wsb,
-                      hipStream_t st) {
+                      hipStream_t st, const GateIn& gate) {
 #define GDN_FWD(KK_, BWD_, OUT_)                                                             \
   launch_chunk<KK_, BWD_, OUT_>(q, k, v, g, beta, h0, ht, o, cu, B, T, Hqk, Hv, V, N, scale, l2, \
-                                p, wsb, st)
+                                p, wsb, st, gate)
   if (K == 128) {
     if (mode == FwdMode::kForward) GDN_FWD(128, false, true);
     else if (mode == FwdMode::kRecompute) GDN_FWD(128, true, false);
@@ -524,6 +529,9 @@ void launch_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
 }  // namespace gdn
 
 namespace gdn_host {
+int validate_gate(const char* name, const void* A_log, const void* dt_bias, int a_dtype,
+                  int b_dtype, int p_dtype, float sp_beta, long long tokens);
+int validate_gate_size(const char* name, long long elements);
 int validate_common(const void* q, const void* k, const void* v, const float* g,
                     const float* beta, const float* h0, const float* ht, const void* o,
                     const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N);
@@ -536,30 +544,68 @@ extern "C" size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K
       .total;
 }
 
+namespace {
+int chunk_fwd_impl(const void* q, const void* k, const void* v, const float* g,
+                   const float* beta, const float* h0, float* ht, void* o,
+                   const int32_t* cu_seqlens, int B, int T, int Hqk, int Hv, int K, int V, int N,
+                   float scale, int use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                   const gdn::GateIn& gate, void* stream, const char* name) {
+  if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
+  const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
+                                     use_qk_l2norm != 0, false);
+  if (!workspace || workspace_bytes < p.total)
+    return gdn_host::fail(GDN_ERR_WORKSPACE, std::string(name) + ": workspace needs " +
+                                                 std::to_string(p.total) + " bytes, got " +
+                                                 std::to_string(workspace_bytes));
+  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
+    return gdn_host::fail(GDN_ERR_SHAPE, std::string(name) + ": problem too large");
+  gdn::launch_chunk_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                        static_cast<const uint16_t*>(v), g, beta, h0, ht,
+                        static_cast<uint16_t*>(o), cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
+                        use_qk_l2norm != 0, gdn::FwdMode::kForward, p,
+                        static_cast<unsigned char*>(workspace), static_cast<hipStream_t>(stream),
+                        gate);
+  return gdn_host::check_launch(name);
+}
+}  // namespace
+
 extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
                              const float* beta, const float* h0, float* ht, void* o,
                              const int32_t* cu_seqlens, int B, int T, int Hqk, int Hv, int K,
                              int V, int N, float scale, int use_qk_l2norm, void* workspace,
                              size_t workspace_bytes, void* stream) {
-  int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk, Hv,
-                                     K, V, N);
+  const int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk,
+                                           Hv, K, V, N);
   if (rc) return rc;
-  if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
-  const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
-                                     use_qk_l2norm != 0, false);
-  if (!workspace || workspace_bytes < p.total)
-    return gdn_host::fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace needs " +
-                                                 std::to_string(p.total) + " bytes, got " +
-                                                 std::to_string(workspace_bytes));
-  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
-    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_fwd: problem too large");
-  gdn::launch_chunk_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                        static_cast<const uint16_t*>(v), g, beta, h0, ht,
-                        static_cast<uint16_t*>(o), cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
-                        use_qk_l2norm != 0, gdn::FwdMode::kForward, p,
-                        static_cast<unsigned char*>(workspace),
-                        static_cast<hipStream_t>(stream));
-  return gdn_host::check_launch("gdn_chunk_fwd");
+  return chunk_fwd_impl(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
+                        use_qk_l2norm, workspace, workspace_bytes, gdn::GateIn{}, stream,
+                        "gdn_chunk_fwd");
+}
+
+// Prefill with the gating computed inside (declared in gdn_layer.h): the prep
+// kernel forms g and beta from (A_log, a, b, dt_bias); no g / beta tensor.
+extern "C" int gdn_chunk_fwd_gating(const void* q, const void* k, const void* v,
+                                    const void* A_log, const void* a, const void* b,
+                                    const void* dt_bias, int a_dtype, int b_dtype, int p_dtype,
+                                    float sp_beta, float sp_threshold, const float* h0,
+                                    float* ht, void* o, const int32_t* cu_seqlens, int B, int T,
+                                    int Hqk, int Hv, int K, int V, int N, float scale,
+                                    int use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  const char* name = "gdn_chunk_fwd_gating";
+  int rc = gdn_host::validate_common(q, k, v, static_cast<const float*>(a),
+                                     static_cast<const float*>(b), h0, ht, o, cu_seqlens, B, T,
+                                     Hqk, Hv, K, V, N);
+  if (rc) return rc;
+  rc = gdn_host::validate_gate(name, A_log, dt_bias, a_dtype, b_dtype, p_dtype, sp_beta,
+                               (long long)B * T);
+  if (rc) return rc;
+  rc = gdn_host::validate_gate_size(name, (long long)B * T * Hv);
+  if (rc) return rc;
+  const gdn::GateIn gate{A_log, a, b, dt_bias, a_dtype, b_dtype, p_dtype, sp_beta, sp_threshold,
+                         (long long)B * T * Hv, Hv};
+  return chunk_fwd_impl(q, k, v, nullptr, nullptr, h0, ht, o, cu_seqlens, B, T, Hqk, Hv, K, V, N,
+                        scale, use_qk_l2norm, workspace, workspace_bytes, gate, stream, name);
 }
 
 // ----------------------------------------------- allocation-free form ----

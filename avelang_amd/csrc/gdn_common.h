@@ -8,6 +8,7 @@
 #include <string>
 
 #include "../../include/gdn.h"
+#include "../../include/gdn_layer.h"
 
 namespace gdn {
 
@@ -75,6 +76,124 @@ __device__ __forceinline__ f32x4 mfma4f32(float a, float b, f32x4 c) {
 }
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// ------------------------------------------------------------ elements ----
+template <int DT>
+struct Elt;
+template <>
+struct Elt<GDN_DTYPE_F32> {
+  using T = float;
+  static constexpr int VEC = 4;
+  static __device__ __forceinline__ float to_f(T v) { return v; }
+  static __device__ __forceinline__ T from_f(float f) { return f; }
+};
+template <>
+struct Elt<GDN_DTYPE_BF16> {
+  using T = uint16_t;
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f(T v) { return bf2f(v); }
+  static __device__ __forceinline__ T from_f(float f) { return f2bf(f); }
+};
+template <>
+struct Elt<GDN_DTYPE_F16> {
+  using T = uint16_t;
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f(T v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+  }
+  static __device__ __forceinline__ T from_f(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+};
+
+template <int DT>
+__device__ __forceinline__ float lde(const void* p, long long i) {
+  return Elt<DT>::to_f(static_cast<const typename Elt<DT>::T*>(p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void ste(void* p, long long i, float v) {
+  static_cast<typename Elt<DT>::T*>(p)[i] = Elt<DT>::from_f(v);
+}
+// value rounded through the element type (identity for fp32)
+template <int DT>
+__device__ __forceinline__ float round_to(float v) {
+  return Elt<DT>::to_f(Elt<DT>::from_f(v));
+}
+
+// Load of a small parameter tensor whose element type is a runtime code.
+__device__ __forceinline__ float ldp(const void* p, long long i, int dt) {
+  if (dt == GDN_DTYPE_F32) return static_cast<const float*>(p)[i];
+  if (dt == GDN_DTYPE_BF16) return lde<GDN_DTYPE_BF16>(p, i);
+  return lde<GDN_DTYPE_F16>(p, i);
+}
+
+
+inline bool dtype_ok(int dt) {
+  return dt == GDN_DTYPE_F32 || dt == GDN_DTYPE_BF16 || dt == GDN_DTYPE_F16;
+}
+
+// Qwen3-Next gating (modeling_qwen3_next.py:650-652) of element i (token-major
+// [.., H]) of v-head h:  g = -exp(A_log[h]) * softplus(a[i] + dt_bias[h]),
+// beta = sigmoid(b[i]); softplus with beta spb and threshold spt as
+// torch.nn.functional.softplus.  One definition for the standalone gating
+// kernel and for the core kernels that compute g and beta themselves, so
+// that both paths give the same bits.
+struct GateIn {
+  const void* A_log;     // [H], element type pdt
+  const void* a;         // [.., H], adt   (NULL: the kernel reads g / beta)
+  const void* b;         // [.., H], bdt   (NULL: beta is not formed)
+  const void* dt_bias;   // [H], pdt
+  int adt, bdt, pdt;
+  float spb, spt;
+  long long n;           // elements of a, b (bounds of the flat loads)
+  int H;                 // elements of A_log, dt_bias
+};
+
+// Element i of an [n] tensor of runtime element type dt, without control
+// flow: a bounded 16-bit and a bounded 32-bit buffer load are both issued
+// and the one the type calls for is selected (the other reads garbage or,
+// past the end, 0).  The same value as ldp; a kernel that keeps loads in
+// flight across this one needs it, since a branch here would make the wait
+// at the join cover every outstanding load.
+__device__ __forceinline__ float ldp_flat(const void* p, long long i, int dt, long long n) {
+  const int es = dt == GDN_DTYPE_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(p), 0, static_cast<int>(n * es), kBufferFlags);
+  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(i * 2), 0, 0);
+  const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(i * 4), 0, 0);
+  const float hf = static_cast<float>(__builtin_bit_cast(_Float16, h));
+  return dt == GDN_DTYPE_F32 ? __uint_as_float(w) : (dt == GDN_DTYPE_BF16 ? bf2f(h) : hf);
+}
+
+// The per-head part (-exp(A_log[h]), dt_bias[h]) and the per-element part,
+// separable so that a kernel walking many tokens of one head forms the
+// first once.  FLAT: loads by ldp_flat (the same values).
+template <bool FLAT = false>
+__device__ __forceinline__ void gate_head(const GateIn& p, int h, float& neg_a, float& dtb) {
+  neg_a = -expf(FLAT ? ldp_flat(p.A_log, h, p.pdt, p.H) : ldp(p.A_log, h, p.pdt));
+  dtb = FLAT ? ldp_flat(p.dt_bias, h, p.pdt, p.H) : ldp(p.dt_bias, h, p.pdt);
+}
+template <bool FLAT = false>
+__device__ __forceinline__ void gate_elem(const GateIn& p, long long i, float neg_a, float dtb,
+                                          float& g, float& beta) {
+  const float av = FLAT ? ldp_flat(p.a, i, p.adt, p.n) : ldp(p.a, i, p.adt);
+  const float bv = FLAT ? ldp_flat(p.b, i, p.bdt, p.n) : (p.b ? ldp(p.b, i, p.bdt) : 0.f);
+  const float x = av + dtb;
+  const float bx = p.spb * x;
+  // both sides formed, then selected (no branch; the clamp changes nothing
+  // where the log side is taken)
+  const float lp = log1pf(expf(fminf(bx, p.spt))) / p.spb;
+  const float sp = bx > p.spt ? x : lp;
+  g = neg_a * sp;
+  beta = 1.f / (1.f + expf(-bv));
+}
+__device__ __forceinline__ void gate_at(const GateIn& p, long long i, int h, float& g,
+                                        float& beta) {
+  float neg_a, dtb;
+  gate_head(p, h, neg_a, dtb);
+  gate_elem(p, i, neg_a, dtb, g, beta);
+}
+
 
 }  // namespace gdn
 

@@ -18,56 +18,6 @@
 
 namespace gdn {
 
-// ------------------------------------------------------------ elements ----
-template <int DT>
-struct Elt;
-template <>
-struct Elt<GDN_DTYPE_F32> {
-  using T = float;
-  static constexpr int VEC = 4;
-  static __device__ __forceinline__ float to_f(T v) { return v; }
-  static __device__ __forceinline__ T from_f(float f) { return f; }
-};
-template <>
-struct Elt<GDN_DTYPE_BF16> {
-  using T = uint16_t;
-  static constexpr int VEC = 8;
-  static __device__ __forceinline__ float to_f(T v) { return bf2f(v); }
-  static __device__ __forceinline__ T from_f(float f) { return f2bf(f); }
-};
-template <>
-struct Elt<GDN_DTYPE_F16> {
-  using T = uint16_t;
-  static constexpr int VEC = 8;
-  static __device__ __forceinline__ float to_f(T v) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, v));
-  }
-  static __device__ __forceinline__ T from_f(float f) {
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
-  }
-};
-
-template <int DT>
-__device__ __forceinline__ float lde(const void* p, long long i) {
-  return Elt<DT>::to_f(static_cast<const typename Elt<DT>::T*>(p)[i]);
-}
-template <int DT>
-__device__ __forceinline__ void ste(void* p, long long i, float v) {
-  static_cast<typename Elt<DT>::T*>(p)[i] = Elt<DT>::from_f(v);
-}
-// value rounded through the element type (identity for fp32)
-template <int DT>
-__device__ __forceinline__ float round_to(float v) {
-  return Elt<DT>::to_f(Elt<DT>::from_f(v));
-}
-
-// Load of a small parameter tensor whose element type is a runtime code.
-__device__ __forceinline__ float ldp(const void* p, long long i, int dt) {
-  if (dt == GDN_DTYPE_F32) return static_cast<const float*>(p)[i];
-  if (dt == GDN_DTYPE_BF16) return lde<GDN_DTYPE_BF16>(p, i);
-  return lde<GDN_DTYPE_F16>(p, i);
-}
-
 // 16-byte vector load / store of VEC consecutive elements (element index
 // aligned to VEC).
 template <int DT>
@@ -120,19 +70,14 @@ __device__ __forceinline__ void ld_params(const void* p, long long e0, int wdt, 
 // -------------------------------------------------------------- gating ----
 // g = -exp(A_log[h]) * softplus(a + dt_bias[h]), beta = sigmoid(b); fp32 math
 // with the accurate exp / log1p (the decay is exponentiated again downstream).
-__global__ __launch_bounds__(256) void gating_kernel(const void* A_log, const void* a,
-                                                     const void* b, const void* dt_bias,
-                                                     float* g, float* beta, long long n, int H,
-                                                     int adt, int bdt, int pdt, float spb,
-                                                     float spt) {
+__global__ __launch_bounds__(256) void gating_kernel(GateIn p, float* g, float* beta, long long n,
+                                                     int H) {
   const long long stride = (long long)gridDim.x * blockDim.x;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const int h = (int)(i % H);
-    const float x = ldp(a, i, adt) + ldp(dt_bias, h, pdt);
-    const float bx = spb * x;
-    const float sp = bx > spt ? x : log1pf(expf(bx)) / spb;
-    g[i] = -expf(ldp(A_log, h, pdt)) * sp;
-    if (beta) beta[i] = 1.f / (1.f + expf(-ldp(b, i, bdt)));
+    float gi, bi;
+    gate_at(p, i, (int)(i % H), gi, bi);
+    g[i] = gi;
+    if (beta) beta[i] = bi;
   }
 }
 
@@ -549,11 +494,10 @@ __global__ __launch_bounds__(256) void conv1d_update_vec_kernel(
 }  // namespace gdn
 
 // ------------------------------------------------------------- host ----
+using gdn::dtype_ok;
+
 namespace {
 
-bool dtype_ok(int dt) {
-  return dt == GDN_DTYPE_F32 || dt == GDN_DTYPE_BF16 || dt == GDN_DTYPE_F16;
-}
 int esize(int dt) { return dt == GDN_DTYPE_F32 ? 4 : 2; }
 int vec_of(int dt) { return dt == GDN_DTYPE_F32 ? 4 : 8; }
 unsigned grid_for(long long n, int per_block) {
@@ -575,9 +519,10 @@ extern "C" int gdn_gating_fwd(const void* A_log, const void* a, const void* b,
   if (n == 0) return GDN_OK;
   if (!A_log || !a || !dt_bias || !g || (beta && !b))
     return gdn_host::fail(GDN_ERR_NULL, "gdn_gating_fwd: A_log, a, dt_bias, g (and b with beta) must be non-NULL");
+  const gdn::GateIn gp{A_log, a, beta ? b : nullptr, dt_bias, a_dtype, b_dtype, p_dtype, sp_beta,
+                       sp_threshold, n, H};
   hipLaunchKernelGGL(gdn::gating_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), A_log, a, b, dt_bias, g, beta, n, H,
-                     a_dtype, b_dtype, p_dtype, sp_beta, sp_threshold);
+                     static_cast<hipStream_t>(stream), gp, g, beta, n, H);
   return gdn_host::check_launch("gdn_gating_fwd");
 }
 

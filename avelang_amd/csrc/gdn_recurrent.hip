@@ -43,7 +43,9 @@ constexpr int kDecodeGrid = GDN_DECODE_GRID;
 // through a buffer resource whose size is 0 for a tile that has nothing to
 // load (past the end, padding slot, no h0): those loads return zeros and
 // touch no memory, so the prefetch needs no branch.
-template <int K, int V, int NT>
+// GATE: g and beta formed in the kernel from `gate`; otherwise read from g /
+// beta.
+template <int K, int V, int NT, bool GATE>
 __global__ __launch_bounds__(NT) void recurrent_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ g,
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     uint16_t* __restrict__ o, const int32_t* __restrict__ cu, int T,
     int total_tokens, int Hqk, int Hv, float scale, int l2norm,
     const int32_t* __restrict__ slots, int num_slots, int ntiles, int slot_stride,
-    const int32_t* __restrict__ accepted) {
+    const int32_t* __restrict__ accepted, GateIn gate) {
   constexpr int COLG = V / 4;          // float4 column groups per row
   constexpr int ROWG = NT / COLG;      // row groups
   constexpr int RPT = K / ROWG;        // rows per lane
@@ -131,8 +133,18 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
       }
       const size_t vh = (size_t)t * Hv + h;
       const u16x4 vb = *reinterpret_cast<const u16x4*>(v + vh * V + 4 * cg);
-      const float gt = g[vh];
-      const float bt = beta[vh];
+      float gt, bt;
+      if constexpr (GATE) {
+        // formed where the other form reads g and beta (a load whose result
+        // is needed at the tile start would wait for the next tile's state
+        // prefetch, issued just before)
+        float neg_a, dtb;
+        gate_head<true>(gate, h, neg_a, dtb);
+        gate_elem<true>(gate, (long long)vh, neg_a, dtb, gt, bt);
+      } else {
+        gt = g[vh];
+        bt = beta[vh];
+      }
       __syncthreads();
 
       float r[NRED];
@@ -230,34 +242,42 @@ static void launch_recurrent(const uint16_t* q, const uint16_t* k, const uint16_
                              float* ht, uint16_t* o, const int32_t* cu, int B, int T,
                              int Hqk, int Hv, int N, float scale, int l2norm,
                              const int32_t* slots, int num_slots, hipStream_t stream,
-                             int slot_stride = 0, const int32_t* accepted = nullptr) {
+                             int slot_stride = 0, const int32_t* accepted = nullptr,
+                             const GateIn& gate = GateIn{}) {
   const int total_tokens = B * T;
   constexpr int NT = (K * V >= 128 * 128) ? 512 : 256;
   const int ntiles = N * Hv;
   // persistent workgroups: enough to fill every CU several times over, each
   // walking ntiles / grid tiles with the next state prefetched
   const int grid = ntiles < kDecodeGrid ? ntiles : kDecodeGrid;
-  hipLaunchKernelGGL((recurrent_kernel<K, V, NT>), dim3(grid), dim3(NT), 0, stream, q, k, v,
-                     g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm, slots,
-                     num_slots, ntiles, slot_stride, accepted);
+  if (gate.a)
+    hipLaunchKernelGGL((recurrent_kernel<K, V, NT, true>), dim3(grid), dim3(NT), 0, stream, q,
+                       k, v, g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm,
+                       slots, num_slots, ntiles, slot_stride, accepted, gate);
+  else
+    hipLaunchKernelGGL((recurrent_kernel<K, V, NT, false>), dim3(grid), dim3(NT), 0, stream, q,
+                       k, v, g, beta, h0, ht, o, cu, T, total_tokens, Hqk, Hv, scale, l2norm,
+                       slots, num_slots, ntiles, slot_stride, accepted, gate);
 }
 
 }  // namespace gdn
 
 namespace gdn_host {
+int validate_gate(const char* name, const void* A_log, const void* dt_bias, int a_dtype,
+                  int b_dtype, int p_dtype, float sp_beta, long long tokens);
+int validate_gate_size(const char* name, long long elements);
 int validate_common(const void* q, const void* k, const void* v, const float* g,
                     const float* beta, const float* h0, const float* ht, const void* o,
                     const int32_t* cu, int B, int T, int Hqk, int Hv, int K, int V, int N);
 }
 
-extern "C" int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
-                                 const float* g, const float* beta, const float* h0,
-                                 float* ht, void* o, const int32_t* cu_seqlens, int B,
-                                 int T, int Hqk, int Hv, int K, int V, int N, float scale,
-                                 int use_qk_l2norm, void* stream) {
-  int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk,
-                                     Hv, K, V, N);
-  if (rc) return rc;
+namespace {
+// gdn_recurrent_fwd and its gating form
+int recurrent_plain(const void* q, const void* k, const void* v, const float* g,
+                    const float* beta, const float* h0, float* ht, void* o,
+                    const int32_t* cu_seqlens, int B, int T, int Hqk, int Hv, int K, int V, int N,
+                    float scale, int use_qk_l2norm, const gdn::GateIn& gate, void* stream,
+                    const char* name) {
   if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
   auto* qq = static_cast<const uint16_t*>(q);
   auto* kk = static_cast<const uint16_t*>(k);
@@ -267,37 +287,34 @@ extern "C" int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
 #define GDN_REC(KK, VV)                                                                   \
   if (K == KK && V == VV) {                                                               \
     gdn::launch_recurrent<KK, VV>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, \
-                                  Hv, N, scale, use_qk_l2norm, nullptr, N, st);           \
-    return gdn_host::check_launch("gdn_recurrent_fwd");                                   \
+                                  Hv, N, scale, use_qk_l2norm, nullptr, N, st, 0, nullptr, \
+                                  gate);                                                  \
+    return gdn_host::check_launch(name);                                                  \
   }
   GDN_REC(128, 128)
   GDN_REC(64, 64)
   GDN_REC(128, 64)
   GDN_REC(64, 128)
 #undef GDN_REC
-  return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd: unsupported K/V");
+  return gdn_host::fail(GDN_ERR_SHAPE, std::string(name) + ": unsupported K/V");
 }
 
-// Continuous batching: sequence n advances state slot state_indices[n] of a
-// [num_slots, Hv, K, V] pool (declared in gdn_layer.h).
-extern "C" int gdn_recurrent_fwd_indexed(const void* q, const void* k, const void* v,
-                                         const float* g, const float* beta, const float* h0,
-                                         float* ht, void* o, const int32_t* cu_seqlens,
-                                         const int32_t* state_indices, int B, int T, int Hqk,
-                                         int Hv, int K, int V, int N, int num_slots,
-                                         float scale, int use_qk_l2norm, void* stream) {
-  int rc = gdn_host::validate_common(q, k, v, g, beta, nullptr, nullptr, o, cu_seqlens, B, T,
-                                     Hqk, Hv, K, V, N);
-  if (rc) return rc;
+// gdn_recurrent_fwd_indexed and the gating form with state indices
+int recurrent_indexed(const void* q, const void* k, const void* v, const float* g,
+                      const float* beta, const float* h0, float* ht, void* o,
+                      const int32_t* cu_seqlens, const int32_t* state_indices, int B, int T,
+                      int Hqk, int Hv, int K, int V, int N, int num_slots, float scale,
+                      int use_qk_l2norm, const gdn::GateIn& gate, void* stream,
+                      const char* name) {
   if (num_slots < 0)
-    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_indexed: num_slots must be >= 0");
+    return gdn_host::fail(GDN_ERR_SHAPE, std::string(name) + ": num_slots must be >= 0");
   if (N > 0 && !state_indices)
-    return gdn_host::fail(GDN_ERR_NULL, "gdn_recurrent_fwd_indexed: state_indices must be non-NULL");
+    return gdn_host::fail(GDN_ERR_NULL, std::string(name) + ": state_indices must be non-NULL");
   if (ht && h0 && ht != h0) {
     const size_t sb = (size_t)num_slots * Hv * K * V * sizeof(float);
     const auto pa = reinterpret_cast<uintptr_t>(h0), pb = reinterpret_cast<uintptr_t>(ht);
     if (pa < pb + sb && pb < pa + sb)
-      return gdn_host::fail(GDN_ERR_ALIAS, "gdn_recurrent_fwd_indexed: ht must equal h0 exactly or not overlap it");
+      return gdn_host::fail(GDN_ERR_ALIAS, std::string(name) + ": ht must equal h0 exactly or not overlap it");
   }
   if (N == 0 || num_slots == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;
   auto* qq = static_cast<const uint16_t*>(q);
@@ -309,15 +326,76 @@ extern "C" int gdn_recurrent_fwd_indexed(const void* q, const void* k, const voi
   if (K == KK && V == VV) {                                                               \
     gdn::launch_recurrent<KK, VV>(qq, kk, vv, g, beta, h0, ht, oo, cu_seqlens, B, T, Hqk, \
                                   Hv, N, scale, use_qk_l2norm, state_indices, num_slots,  \
-                                  st);                                                    \
-    return gdn_host::check_launch("gdn_recurrent_fwd_indexed");                           \
+                                  st, 0, nullptr, gate);                                  \
+    return gdn_host::check_launch(name);                                                  \
   }
   GDN_RECI(128, 128)
   GDN_RECI(64, 64)
   GDN_RECI(128, 64)
   GDN_RECI(64, 128)
 #undef GDN_RECI
-  return gdn_host::fail(GDN_ERR_SHAPE, "gdn_recurrent_fwd_indexed: unsupported K/V");
+  return gdn_host::fail(GDN_ERR_SHAPE, std::string(name) + ": unsupported K/V");
+}
+}  // namespace
+
+extern "C" int gdn_recurrent_fwd(const void* q, const void* k, const void* v,
+                                 const float* g, const float* beta, const float* h0,
+                                 float* ht, void* o, const int32_t* cu_seqlens, int B,
+                                 int T, int Hqk, int Hv, int K, int V, int N, float scale,
+                                 int use_qk_l2norm, void* stream) {
+  const int rc = gdn_host::validate_common(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk,
+                                           Hv, K, V, N);
+  if (rc) return rc;
+  return recurrent_plain(q, k, v, g, beta, h0, ht, o, cu_seqlens, B, T, Hqk, Hv, K, V, N, scale,
+                         use_qk_l2norm, gdn::GateIn{}, stream, "gdn_recurrent_fwd");
+}
+
+// Continuous batching: sequence n advances state slot state_indices[n] of a
+// [num_slots, Hv, K, V] pool (declared in gdn_layer.h).
+extern "C" int gdn_recurrent_fwd_indexed(const void* q, const void* k, const void* v,
+                                         const float* g, const float* beta, const float* h0,
+                                         float* ht, void* o, const int32_t* cu_seqlens,
+                                         const int32_t* state_indices, int B, int T, int Hqk,
+                                         int Hv, int K, int V, int N, int num_slots,
+                                         float scale, int use_qk_l2norm, void* stream) {
+  const int rc = gdn_host::validate_common(q, k, v, g, beta, nullptr, nullptr, o, cu_seqlens,
+                                           B, T, Hqk, Hv, K, V, N);
+  if (rc) return rc;
+  return recurrent_indexed(q, k, v, g, beta, h0, ht, o, cu_seqlens, state_indices, B, T, Hqk,
+                           Hv, K, V, N, num_slots, scale, use_qk_l2norm, gdn::GateIn{}, stream,
+                           "gdn_recurrent_fwd_indexed");
+}
+
+// Decode with the gating computed inside (declared in gdn_layer.h): g and
+// beta come from (A_log, a, b, dt_bias) in the kernel, not from HBM.
+extern "C" int gdn_recurrent_fwd_gating(const void* q, const void* k, const void* v,
+                                        const void* A_log, const void* a, const void* b,
+                                        const void* dt_bias, int a_dtype, int b_dtype,
+                                        int p_dtype, float sp_beta, float sp_threshold,
+                                        const float* h0, float* ht, void* o,
+                                        const int32_t* cu_seqlens, const int32_t* state_indices,
+                                        int B, int T, int Hqk, int Hv, int K, int V, int N,
+                                        int num_slots, float scale, int use_qk_l2norm,
+                                        void* stream) {
+  const char* name = "gdn_recurrent_fwd_gating";
+  int rc = gdn_host::validate_common(q, k, v, static_cast<const float*>(a),
+                                     static_cast<const float*>(b), state_indices ? nullptr : h0,
+                                     state_indices ? nullptr : ht, o, cu_seqlens, B, T, Hqk, Hv,
+                                     K, V, N);
+  if (rc) return rc;
+  rc = gdn_host::validate_gate(name, A_log, dt_bias, a_dtype, b_dtype, p_dtype, sp_beta,
+                               (long long)B * T);
+  if (rc) return rc;
+  rc = gdn_host::validate_gate_size(name, (long long)B * T * Hv);
+  if (rc) return rc;
+  const gdn::GateIn gate{A_log, a, b, dt_bias, a_dtype, b_dtype, p_dtype, sp_beta, sp_threshold,
+                         (long long)B * T * Hv, Hv};
+  if (state_indices)
+    return recurrent_indexed(q, k, v, nullptr, nullptr, h0, ht, o, cu_seqlens, state_indices, B,
+                             T, Hqk, Hv, K, V, N, num_slots, scale, use_qk_l2norm, gate, stream,
+                             name);
+  return recurrent_plain(q, k, v, nullptr, nullptr, h0, ht, o, cu_seqlens, B, T, Hqk, Hv, K, V,
+                         N, scale, use_qk_l2norm, gate, stream, name);
 }
 
 // Speculative decoding over a state pool (declared in gdn_layer.h): per-token

@@ -31,6 +31,8 @@ __all__ = [
     "chunk_gated_delta_rule_fwd_save",
     "fused_recurrent_gated_delta_rule",
     "chunk_workspace_bytes",
+    "chunk_gated_delta_rule_gated",
+    "fused_recurrent_gated_delta_rule_gated",
     "chunk_bwd_workspace_bytes",
 ]
 
@@ -46,7 +48,7 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def _check_inputs(q, k, v, g, beta, initial_state, cu_seqlens, name):
+def _check_inputs(q, k, v, g, beta, initial_state, cu_seqlens, name, convert_gates=True):
     for nm, t in (("q", q), ("k", k), ("v", v)):
         if not isinstance(t, torch.Tensor):
             raise ValueError(f"{name}: {nm} must be a torch.Tensor")
@@ -110,8 +112,11 @@ def _check_inputs(q, k, v, g, beta, initial_state, cu_seqlens, name):
             raise ValueError(f"{name}: initial_state must be torch.float32, got {initial_state.dtype}.")
         if initial_state.device != dev:
             raise ValueError(f"{name}: initial_state must be on {dev}.")
-    g = g.to(torch.float32).contiguous()
-    beta = beta.to(torch.float32).contiguous()
+    if convert_gates:
+        g = g.to(torch.float32).contiguous()
+        beta = beta.to(torch.float32).contiguous()
+    else:   # the gating inputs a, b of the fused entry points, in their own dtype
+        g, beta = g.contiguous(), beta.contiguous()
     return (q.contiguous(), k.contiguous(), v.contiguous(), g, beta, cu,
             (B, T, Hqk, Hv, K, V, N))
 
@@ -328,12 +333,12 @@ def chunk_gated_delta_rule(
 
 def _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
                use_qk_l2norm_in_kernel, workspace=None, out=None, final_state=None,
-               save_workspace=None):
+               save_workspace=None, gate=None, name="chunk_gated_delta_rule"):
     """gdn_chunk_fwd, or gdn_chunk_fwd_save into ``save_workspace`` (a
-    backward-sized workspace the backward then reuses)."""
-    name = "chunk_gated_delta_rule"
+    backward-sized workspace the backward then reuses), or with ``gate``
+    gdn_chunk_fwd_gating (g, beta are then the gating inputs a, b)."""
     q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
-        q, k, v, g, beta, initial_state, cu_seqlens, name)
+        q, k, v, g, beta, initial_state, cu_seqlens, name, convert_gates=gate is None)
     if scale is None:
         scale = K ** -0.5
     dev = q.device
@@ -362,6 +367,15 @@ def _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_se
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     elif workspace.numel() * workspace.element_size() < nbytes or workspace.device != dev:
         raise ValueError(f"{name}: workspace must be >= {nbytes} bytes on {dev}.")
+    if gate is not None:
+        rc = _native.lib().gdn_chunk_fwd_gating(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), *_gate_ptrs(gate, g, beta, Hv, dev, name),
+            _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
+            B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            _stream_ptr(dev))
+        _native.check(rc, name)
+        return o, ht
     rc = entry(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
         _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
@@ -425,8 +439,14 @@ def fused_recurrent_gated_delta_rule(
         return _recurrent_indexed(q, k, v, g, beta, scale, initial_state, output_final_state,
                                   cu_seqlens, use_qk_l2norm_in_kernel, inplace_final_state,
                                   ssm_state_indices, out, name)
+    return _recurrent_plain(q, k, v, g, beta, scale, initial_state, output_final_state,
+                            cu_seqlens, use_qk_l2norm_in_kernel, inplace_final_state, out, name)
+
+
+def _recurrent_plain(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
+                     use_qk_l2norm_in_kernel, inplace_final_state, out, name, gate=None):
     q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
-        q, k, v, g, beta, initial_state, cu_seqlens, name)
+        q, k, v, g, beta, initial_state, cu_seqlens, name, convert_gates=gate is None)
     if scale is None:
         scale = K ** -0.5
     dev = q.device
@@ -444,24 +464,31 @@ def fused_recurrent_gated_delta_rule(
             ht = h0
         else:
             ht = torch.empty((N, Hv, K, V), dtype=torch.float32, device=dev)
-    rc = _native.lib().gdn_recurrent_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
-        _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
-        B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
-        _stream_ptr(dev))
+    if gate is not None:
+        rc = _native.lib().gdn_recurrent_fwd_gating(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), *_gate_ptrs(gate, g, beta, Hv, dev, name),
+            _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu), None,
+            B, T, Hqk, Hv, K, V, N, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+            _stream_ptr(dev))
+    else:
+        rc = _native.lib().gdn_recurrent_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+            _ptr(h0), _ptr(ht), o.data_ptr(), _ptr(cu),
+            B, T, Hqk, Hv, K, V, N, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+            _stream_ptr(dev))
     _native.check(rc, name)
     return o, ht
 
 
 def _recurrent_indexed(q, k, v, g, beta, scale, pool, output_final_state, cu_seqlens,
-                       use_qk_l2norm_in_kernel, inplace_final_state, idx, out, name):
+                       use_qk_l2norm_in_kernel, inplace_final_state, idx, out, name, gate=None):
     if pool is None or not isinstance(pool, torch.Tensor) or pool.dim() != 4:
         raise ValueError(f"{name}: ssm_state_indices requires initial_state as a state pool "
                          "[num_slots, Hv, K, V].")
     if output_final_state and not inplace_final_state:
         raise ValueError(f"{name}: with ssm_state_indices the final state is written in place.")
     q, k, v, g, beta, cu, (B, T, Hqk, Hv, K, V, N) = _check_inputs(
-        q, k, v, g, beta, None, cu_seqlens, name)
+        q, k, v, g, beta, None, cu_seqlens, name, convert_gates=gate is None)
     dev = q.device
     if (tuple(pool.shape[1:]) != (Hv, K, V) or pool.dtype != torch.float32
             or pool.device != dev or not pool.is_contiguous()):
@@ -479,11 +506,18 @@ def _recurrent_indexed(q, k, v, g, beta, scale, pool, output_final_state, cu_seq
     if o.shape != v.shape or o.dtype != torch.bfloat16 or o.device != dev or not o.is_contiguous():
         raise ValueError(f"{name}: out must be a contiguous bf16 tensor of shape {tuple(v.shape)}.")
     ht = pool if output_final_state else None
-    rc = _native.lib().gdn_recurrent_fwd_indexed(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
-        pool.data_ptr(), _ptr(ht), o.data_ptr(), _ptr(cu), idx.contiguous().data_ptr(),
-        B, T, Hqk, Hv, K, V, N, pool.shape[0], float(scale),
-        int(bool(use_qk_l2norm_in_kernel)), _stream_ptr(dev))
+    if gate is not None:
+        rc = _native.lib().gdn_recurrent_fwd_gating(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), *_gate_ptrs(gate, g, beta, Hv, dev, name),
+            pool.data_ptr(), _ptr(ht), o.data_ptr(), _ptr(cu), idx.contiguous().data_ptr(),
+            B, T, Hqk, Hv, K, V, N, pool.shape[0], float(scale),
+            int(bool(use_qk_l2norm_in_kernel)), _stream_ptr(dev))
+    else:
+        rc = _native.lib().gdn_recurrent_fwd_indexed(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+            pool.data_ptr(), _ptr(ht), o.data_ptr(), _ptr(cu), idx.contiguous().data_ptr(),
+            B, T, Hqk, Hv, K, V, N, pool.shape[0], float(scale),
+            int(bool(use_qk_l2norm_in_kernel)), _stream_ptr(dev))
     _native.check(rc, name)
     return o, ht
 
@@ -537,3 +571,92 @@ def _recurrent_spec(q, k, v, g, beta, scale, pool, cu_seqlens, use_qk_l2norm_in_
         int(bool(use_qk_l2norm_in_kernel)), _stream_ptr(dev))
     _native.check(rc, name)
     return o, pool
+
+
+# ------------------------------------------------ gating fused into the core
+def _gate_ptrs(gate, a, b, Hv, dev, name):
+    """Pointer / code arguments of the *_gating entry points, after checking
+    A_log, dt_bias ([Hv], one dtype) and the gating inputs a, b."""
+    from .layer_ops import _dt
+    A_log, dt_bias, spb, spt = gate
+    for nm, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+        if not isinstance(t, torch.Tensor) or tuple(t.shape) != (Hv,) or t.device != dev:
+            raise ValueError(f"{name}: {nm} must be a tensor of shape ({Hv},) on {dev}.")
+    if A_log.dtype != dt_bias.dtype:
+        raise ValueError(f"{name}: A_log and dt_bias must share a dtype.")
+    if not spb > 0:
+        raise ValueError(f"{name}: softplus beta must be > 0.")
+    adt, bdt, pdt = _dt(a, name, "a"), _dt(b, name, "b"), _dt(A_log, name, "A_log")
+    return (A_log.contiguous().data_ptr(), a.data_ptr(), b.data_ptr(),
+            dt_bias.contiguous().data_ptr(), adt, bdt, pdt, float(spb), float(spt))
+
+
+def chunk_gated_delta_rule_gated(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    softplus_beta: float = 1.0,
+    softplus_threshold: float = 20.0,
+    *,
+    workspace: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """``chunk_gated_delta_rule`` with the layer's gating fused in.
+
+    The Qwen3-Next layer forms ``g = -exp(A_log) * softplus(a + dt_bias)``
+    and ``beta = sigmoid(b)`` (modeling_qwen3_next.py:650-652) and passes
+    them to the core (:672-683).  Here the core's prep kernel forms them
+    itself from ``a``, ``b`` ([B, T, Hv], bf16 / fp16 / fp32) and ``A_log``,
+    ``dt_bias`` ([Hv]) -- the same definition as ``fused_gdn_gating``, so the
+    result equals ``chunk_gated_delta_rule(q, k, v, *fused_gdn_gating(...))``
+    bit for bit -- and no fp32 g / beta tensor exists.  Forward only.
+    """
+    return _chunk_fwd(q, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens,
+                      use_qk_l2norm_in_kernel, workspace=workspace, out=out,
+                      gate=(A_log, dt_bias, softplus_beta, softplus_threshold),
+                      name="chunk_gated_delta_rule_gated")
+
+
+def fused_recurrent_gated_delta_rule_gated(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    inplace_final_state: bool = True,
+    ssm_state_indices: Optional[torch.Tensor] = None,
+    softplus_beta: float = 1.0,
+    softplus_threshold: float = 20.0,
+    *,
+    out: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """``fused_recurrent_gated_delta_rule`` (plain, or over a slot pool with a
+    1-D ``ssm_state_indices``) with the layer's gating fused in: the decode
+    kernel forms g and beta from ``a``, ``b``, ``A_log``, ``dt_bias`` per
+    token (see ``chunk_gated_delta_rule_gated``)."""
+    name = "fused_recurrent_gated_delta_rule_gated"
+    gate = (A_log, dt_bias, softplus_beta, softplus_threshold)
+    if ssm_state_indices is not None:
+        if ssm_state_indices.dim() != 1:
+            raise ValueError(f"{name}: ssm_state_indices must be 1-D [N].")
+        return _recurrent_indexed(q, k, v, a, b, scale, initial_state, output_final_state,
+                                  cu_seqlens, use_qk_l2norm_in_kernel, inplace_final_state,
+                                  ssm_state_indices, out, name, gate=gate)
+    return _recurrent_plain(q, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens,
+                            use_qk_l2norm_in_kernel, inplace_final_state, out, name, gate=gate)

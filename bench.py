@@ -309,6 +309,74 @@ def _time_graph(dev, fn, launches=20, reps=5):
     return float(np.median(times))
 
 
+def bench_fusions(dev):
+    """The layer's gating fused into the core against the two-step sequence
+    (fused_gdn_gating, then the core), per layer call: config 1 prefill and
+    config 2 decode (state in place), a / b bf16 [B, T, Hv], A_log / dt_bias
+    fp32.  Bytes saved per (token, v-head): the gating kernel's a, b reads
+    (4) and g, beta writes (8), and the core's g, beta reads (8), less the
+    fused core's a, b reads (4) = 16."""
+    from avelang_amd import (chunk_gated_delta_rule, chunk_gated_delta_rule_gated,
+                             chunk_workspace_bytes, fused_gdn_gating,
+                             fused_recurrent_gated_delta_rule,
+                             fused_recurrent_gated_delta_rule_gated)
+    from avelang_amd import workloads as W
+
+    def gates(B, T, Hv, seed):
+        gen = torch.Generator(device="cpu").manual_seed(seed)
+        a = torch.randn((B, T, Hv), generator=gen).to(dev, torch.bfloat16)
+        b = torch.randn((B, T, Hv), generator=gen).to(dev, torch.bfloat16)
+        A_log = torch.log(torch.empty(Hv).uniform_(0.5, 8.0, generator=gen)).to(dev)
+        dt_bias = torch.ones(Hv, device=dev)
+        return a, b, A_log, dt_bias
+
+    out = {}
+    wl = W.config("cfg1_prefill_qwen3next", seed=1)
+    d = wl.dims
+    t = wl.torch(dev)
+    B, T, Hqk, Hv, K, V, N = (d[x] for x in ("B", "T", "Hqk", "Hv", "K", "V", "N"))
+    a, b, A_log, dt_bias = gates(B, T, Hv, 5)
+    ws = torch.empty(chunk_workspace_bytes(B, T, Hqk, Hv, K, V, N, False, False),
+                     dtype=torch.uint8, device=dev)
+    o = torch.empty_like(t["v"])
+    kw = dict(initial_state=t["initial_state"], output_final_state=True, workspace=ws, out=o)
+
+    def two_step():
+        g, beta = fused_gdn_gating(A_log, a, b, dt_bias)
+        chunk_gated_delta_rule(t["q"], t["k"], t["v"], g, beta, **kw)
+
+    def fused():
+        chunk_gated_delta_rule_gated(t["q"], t["k"], t["v"], a, b, A_log, dt_bias, **kw)
+
+    ms2, ms1 = _time_graph(dev, two_step, launches=10), _time_graph(dev, fused, launches=10)
+    out["prefill_cfg1"] = {"two_step_us": round(ms2 * 1e3, 2), "fused_us": round(ms1 * 1e3, 2),
+                           "saved_us": round((ms2 - ms1) * 1e3, 2),
+                           "hbm_bytes_saved": 16 * B * T * Hv}
+    wl = W.config("cfg2_decode_b256", seed=2)
+    d = wl.dims
+    t = wl.torch(dev)
+    B, T, Hqk, Hv, K, V, N = (d[x] for x in ("B", "T", "Hqk", "Hv", "K", "V", "N"))
+    a, b, A_log, dt_bias = gates(B, T, Hv, 6)
+    state = t["initial_state"].clone()
+    o = torch.empty_like(t["v"])
+
+    def two_step_dec():
+        g, beta = fused_gdn_gating(A_log, a, b, dt_bias)
+        fused_recurrent_gated_delta_rule(t["q"], t["k"], t["v"], g, beta, initial_state=state,
+                                         output_final_state=True, out=o)
+
+    def fused_dec():
+        fused_recurrent_gated_delta_rule_gated(t["q"], t["k"], t["v"], a, b, A_log, dt_bias,
+                                               initial_state=state, output_final_state=True,
+                                               out=o)
+
+    ms2, ms1 = _time_graph(dev, two_step_dec), _time_graph(dev, fused_dec)
+    out["decode_cfg2"] = {"two_step_us": round(ms2 * 1e3, 2), "fused_us": round(ms1 * 1e3, 2),
+                          "saved_us": round((ms2 - ms1) * 1e3, 2),
+                          "hbm_bytes_saved": 16 * B * T * Hv}
+    return out
+
+
 def bench_layer_ops(dev):
     """The layer's neighbours of the core at the Qwen3-Next layer shape
     (T = 8192, conv_dim = 2 * 16 * 128 + 32 * 128 = 8192; decode batch 256),
@@ -623,6 +691,7 @@ def main():
     dec = bench_decode(dev, args.decode_steps)
     extra = not args.headline_only
     layer = bench_layer_ops(dev) if extra and not args.no_layer_ops else None
+    fusions = bench_fusions(dev) if extra and not args.no_layer_ops else None
     pre_l2 = bench_prefill(dev, max(args.steps // 2, 1), args.warmup, l2norm=True) if extra else None
     others = ([bench_prefill_config(dev, n) for n in ("cfg3_varlen_64seq", "cfg4_long_context")]
               if extra else None)
@@ -681,6 +750,7 @@ def main():
         "prefill_other_configs": others,
         "backward": None if bwd is None else _backward_record(bwd, args.no_cpu),
         "layer_ops": layer,
+        "fusions": fusions,
         "host_wall_ms_per_step": round(pre["wall_ms"], 5),
     }
     print(json.dumps(rec), flush=True)

@@ -148,6 +148,38 @@ int gdn_recurrent_fwd_spec(const void* q, const void* k, const void* v,
                            int B, int T, int Hqk, int Hv, int K, int V, int N,
                            int num_slots, float scale, int use_qk_l2norm, void* stream);
 
+/*
+ * The gating fused into the core (TF:650-652 feeding :658-683): g and beta
+ * are formed from (A_log, a, b, dt_bias) inside the kernels exactly as
+ * gdn_gating_fwd forms them (one shared definition, the same bits), so no
+ * fp32 g / beta tensor is written and read back, and the gating launch
+ * goes away.  Arguments as gdn_gating_fwd's (a, b [B, T, Hv]) followed by
+ * the core's.  No counterpart in the reference (it has no GDN code); the
+ * layer's own call sequence gating -> core is what they replace.
+ *
+ * gdn_chunk_fwd_gating: gdn_chunk_fwd with g, beta replaced; workspace of
+ *   gdn_chunk_workspace_bytes.
+ * gdn_recurrent_fwd_gating: state_indices NULL: gdn_recurrent_fwd (h0 ->
+ *   ht, num_slots ignored); state_indices set: gdn_recurrent_fwd_indexed
+ *   (h0 / ht are the [num_slots, Hv, K, V] pool).
+ */
+int gdn_chunk_fwd_gating(const void* q, const void* k, const void* v,
+                         const void* A_log, const void* a, const void* b, const void* dt_bias,
+                         int a_dtype, int b_dtype, int p_dtype, float sp_beta,
+                         float sp_threshold,
+                         const float* h0, float* ht, void* o, const int32_t* cu_seqlens,
+                         int B, int T, int Hqk, int Hv, int K, int V, int N,
+                         float scale, int use_qk_l2norm,
+                         void* workspace, size_t workspace_bytes, void* stream);
+int gdn_recurrent_fwd_gating(const void* q, const void* k, const void* v,
+                             const void* A_log, const void* a, const void* b,
+                             const void* dt_bias, int a_dtype, int b_dtype, int p_dtype,
+                             float sp_beta, float sp_threshold,
+                             const float* h0, float* ht, void* o, const int32_t* cu_seqlens,
+                             const int32_t* state_indices,
+                             int B, int T, int Hqk, int Hv, int K, int V, int N, int num_slots,
+                             float scale, int use_qk_l2norm, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,9 +32,9 @@ def test_header_declares_expected_entry_points():
                                      "gdn_chunk_workspace_bytes", "gdn_cu_seqlens_check",
                                      "gdn_last_error", "gdn_recurrent_fwd"]
     assert _declared(("gdn_layer.h",)) == [
-        "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_gating_fwd",
-        "gdn_l2norm_fwd", "gdn_recurrent_fwd_indexed", "gdn_recurrent_fwd_spec",
-        "gdn_rmsnorm_gated_fwd"]
+        "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_chunk_fwd_gating",
+        "gdn_gating_fwd", "gdn_l2norm_fwd", "gdn_recurrent_fwd_gating",
+        "gdn_recurrent_fwd_indexed", "gdn_recurrent_fwd_spec", "gdn_rmsnorm_gated_fwd"]
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -302,3 +302,19 @@ def test_noalloc_scratch_limit_checked_before_launch(lib):
     assert lib.gdn_chunk_fwd_noalloc(*fake, 1, 8192, 16, 32, 128, 128, 1, 0.1, 0, None) == -4
     assert "scratch" in lib.gdn_last_error().decode()
     assert lib.gdn_chunk_fwd_noalloc(None, *fake[1:], 1, 64, 2, 4, 128, 128, 1, 0.1, 0, None) == -1
+
+
+def test_fused_gating_argument_errors(lib):
+    """The *_gating entry points check the gating arguments before launching."""
+    P = [1 << 28, 2 << 28, 3 << 28]                       # q, k, v
+    G = [4 << 28, 5 << 28, 6 << 28, 7 << 28]              # A_log, a, b, dt_bias
+    tail = [None, None, 8 << 28, None, 1, 64, 2, 4, 128, 128, 1, 0.1, 0]
+    ws = [9 << 28, 1 << 30, None]
+    assert lib.gdn_chunk_fwd_gating(*P, *G, 7, 1, 0, 1.0, 20.0, *tail, *ws) == -2
+    assert "dtype" in lib.gdn_last_error().decode()
+    assert lib.gdn_chunk_fwd_gating(*P, *G, 1, 1, 0, 0.0, 20.0, *tail, *ws) == -2
+    assert lib.gdn_chunk_fwd_gating(*P, None, *G[1:], 1, 1, 0, 1.0, 20.0, *tail, *ws) == -1
+    assert lib.gdn_chunk_fwd_gating(*P, G[0], None, *G[2:], 1, 1, 0, 1.0, 20.0, *tail, *ws) == -1
+    rtail = [None, None, 8 << 28, None, None, 1, 4, 2, 4, 128, 128, 1, 1, 0.1, 0, None]
+    assert lib.gdn_recurrent_fwd_gating(*P, *G[:3], None, 1, 1, 0, 1.0, 20.0, *rtail) == -1
+    assert lib.gdn_recurrent_fwd_gating(*P, *G, 1, 1, 9, 1.0, 20.0, *rtail) == -2
