@@ -363,7 +363,7 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
     // exact count.
     constexpr int kQP = OUT ? 4 * KB + 6 : 0;   // Q / P loads per chunk
     constexpr int kVG = 3;                      // V tile (2) + G (1)
-    constexpr int kSave = SAVE ? KB + 16 : 0;   // state and delta stores per chunk
+    constexpr int kSave = SAVE ? KB + 2 : 0;    // state and delta stores per chunk
     constexpr int kStep = (OUT ? 4 : 0) + kSave + kQP + kVG;   // stores + loads per step
     const int rowq = Hqk * K * 2;
     struct Regs {
@@ -455,15 +455,25 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
         for (int b = 0; b < KB; ++b)
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sh[b]), hr,
                                                  ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
+        // deltas: lane t gathers token row t (its 16 columns) from the vnew
+        // fragments in LDS -- element (t % 8) of fragment lane 16 ((t / 8) % 4)
+        // + n of k-block t / 32 -- and writes it with two 16-byte stores
         const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
             ws.dl + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+        u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
+        if (live) {
+          const uint16_t* src =
+              reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
+              (lane & 7);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_raw_buffer_store_b16(
-                vx[b][i], dr, (((32 * b + 8 * grp + i) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
+          for (int c = 0; c < 8; ++c) {
+            d0[c] = src[8 * c];
+            d1[c] = src[8 * (c + 8)];
+          }
         }
+        const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr, drow, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), dr, drow + 16, 0, 0);
       }
       if constexpr (!OUT) return;
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
