@@ -22,6 +22,8 @@ struct ChunkWs {
   float* tmat;      // [NC][Hv][64][64] T = (I + A)^-1 (fp32, row-major, upper part 0)
   u16x8* ttfrag;    // [NC][Hv][4][2][2][64] A-operand fragments of Tb^T (hi, lo)
   u16x8* ptfrag;    // [NC][Hv][4][2][64]    A-operand fragments of P^T
+  u16x8* qtfrag;    // [NC][Hqk][K/16][2][64] A-operand fragments of Q^T (key-row tile,
+                    // token k-block; the l2-normalised q with use_qk_l2norm)
   uint16_t* hs;     // [NC][Hv][V][K] bf16: state at the start of every chunk, transposed
   uint16_t* dl;     // [B*T][Hv][V]   bf16: d = vnew, the per-token delta
 };
@@ -82,11 +84,51 @@ __device__ __forceinline__ u16x8 lds_colfrag(const uint16_t* X, int ld, int k0, 
   return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// ------------------------------------------- state-wave chain helpers ----
+// (the forward chain gdn_chunk_chain.hip and the reverse chain
+// gdn_chunk_rev.hip)
+
+// rho of tile row 16 T + m (m < 16)
+__device__ __forceinline__ int rho_row(int T, int m) {
+  return 32 * (T >> 1) + 8 * (m >> 2) + 4 * (T & 1) + (m & 3);
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u16x8 cat8(u16x4 a, u16x4 b) {
+  return u16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Tb fragment slot of (row tile ti, k-block b): row tiles 0 and 1 have no
+// k-block 1 (Tb is lower triangular), so six slots per hi / lo part.
+__device__ __forceinline__ constexpr int tb_slot(int ti, int b) { return b == 0 ? ti : 2 + ti; }
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n
+// vector-memory operations are outstanding, and for nothing else.
+__device__ __forceinline__ constexpr int vmcnt_imm(int n) {
+  return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14);
+}
+
+// Staged K rows: row stride 2K + 16 bytes and 64 more bytes after every 16
+// rows.  The column-fragment reads of the state wave (16 rows rho(16 ti +
+// m), one 16-byte piece) then fall on distinct banks, and every K read is a
+// per-lane base plus a compile-time offset.
+template <int K>
+struct KLayout {
+  static constexpr int RS = 2 * K + 16;            // row stride (bytes)
+  static constexpr int GP = 64;                    // extra bytes per 16 rows
+  static constexpr int GU = (16 * RS + GP) / 16;   // 16-byte units per 16 rows
+  static constexpr int UNITS = 4 * GU;             // units of the 64 rows
+  static constexpr int LOADS = (UNITS + 63) / 64;  // 1 KiB direct-to-LDS loads
+  static constexpr int BYTES = LOADS * 1024;       // buffer size
+  __device__ static constexpr int row(int r) { return r * RS + (r >> 4) * GP; }
+};
+
 // Workspace plan (byte offsets into the caller's buffer).
 struct WsPlan {
   size_t off, status, gate, tfrag, pfrag, qn, kn, total;
   // backward only (0 when not planned)
-  size_t tmat, ttfrag, ptfrag, hs, dl, dse, dd;
+  size_t tmat, ttfrag, ptfrag, qtfrag, hs, dl, dse, dd;
   long long ncmax;
 };
 
@@ -113,5 +155,13 @@ template <int K, bool SAVE, bool OUT>
 void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
                      float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
                      int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st);
+
+// Reverse chain of the backward (gdn_chunk_rev.hip): dS' of every chunk into
+// dse, dd into dd, dh0.
+template <int K>
+void launch_rev_sw(const uint16_t* k, const uint16_t* dO, const float* dht, float* dh0,
+                   const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
+                   float scale, const ChunkWs& ws, uint16_t* dse, uint16_t* dd, hipStream_t st);
+
 
 }  // namespace gdn

@@ -313,6 +313,27 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   }
   __syncthreads();
 
+  if constexpr (BWD) {
+    // A-operand fragments of Q^T for the reverse chain (key-row tile T,
+    // token k-block b; lane (r16, grp) holds Q[32 b + 8 grp + i][16 T + r16]),
+    // once per qk-head: the chunk's Q rows pass through the K staging space,
+    // free after K K^T, and each wave gathers key-row tiles w, w + 4, ...
+    if (h % (Hv / Hqk) == 0) {
+#pragma unroll
+      for (int b = 0; b < KB; ++b)
+        *reinterpret_cast<u16x8*>(&Ks[16 * w + r16][32 * b + 8 * grp]) = qa[b];
+      __syncthreads();
+      const size_t qb = ((size_t)ci * Hqk + hq) * (K / 16);
+#pragma unroll
+      for (int T = w; T < K / 16; T += 4) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          ws.qtfrag[((qb + T) * 2 + b) * 64 + lane] = lds_colfrag(&Ks[0][0], K + 8, 32 * b, 16 * T, lane);
+      }
+      __syncthreads();
+    }
+  }
+
   // (I + A)^-1, blocked by 16.  Diagonal blocks: right-looking elimination,
   // lane c < 16 owns column c (15 dependent levels, not 120).
   if (lane < 16) {
@@ -451,6 +472,7 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
     p.tmat = take(nch * 64 * 64 * 4);
     p.ttfrag = take(nch * 4 * 2 * 2 * 64 * 16);
     p.ptfrag = take(nch * 4 * 2 * 64 * 16);
+    p.qtfrag = take((size_t)p.ncmax * Hqk * (K / 16) * 2 * 64 * 16);
     p.hs = take(nch * K * V * 2);
     p.dse = take(nch * K * V * 2);
     p.dl = take((size_t)total * Hv * V * 2);
@@ -473,6 +495,7 @@ ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb) {
     ws.tmat = reinterpret_cast<float*>(wsb + p.tmat);
     ws.ttfrag = reinterpret_cast<u16x8*>(wsb + p.ttfrag);
     ws.ptfrag = reinterpret_cast<u16x8*>(wsb + p.ptfrag);
+    ws.qtfrag = reinterpret_cast<u16x8*>(wsb + p.qtfrag);
     ws.hs = reinterpret_cast<uint16_t*>(wsb + p.hs);
     ws.dl = reinterpret_cast<uint16_t*>(wsb + p.dl);
   }

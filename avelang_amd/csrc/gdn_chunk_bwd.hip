@@ -14,13 +14,13 @@
 // and every gradient of the chunk is local given S, dS', d and dd.
 //
 // Launches (after the forward's chunk table + prep in backward mode, which
-// also writes T, Tb^T and P^T, and the forward chain in save mode, which
-// stores S at every chunk start and d):
-//   chunk_rev_kernel    one workgroup per (sequence, v-head, 16-column V
-//                       tile), reverse over the sequence's chunks; dS' in
-//                       VGPRs (fp32), every product a 16x16x32 bf16 MFMA with
-//                       hi+lo splits where it feeds dS (as the forward chain);
-//                       stores dS' of every chunk and dd (bf16) and dh0
+// also writes T and the fragments of Tb^T, P^T and Q^T, and the forward
+// chain in save mode, which stores S at every chunk start and d):
+//   chunk_rev_sw_kernel (gdn_chunk_rev.hip) one workgroup per (sequence,
+//                       v-head, 16-column V tile), reverse over the
+//                       sequence's chunks; dS' in one wave's VGPRs (fp32),
+//                       hi+lo splits where a product feeds dS (as the forward
+//                       chain); stores dS' of every chunk and dd (bf16) and dh0
 //   chunk_grad_kernel   one workgroup per (chunk, qk-head), fully parallel:
 //                       the local gradients of the group's v-heads, dq / dk
 //                       summed over the group in registers
@@ -35,320 +35,6 @@ struct BwdWs {
   uint16_t* dse;          // [NC][Hv][V][K] bf16: dL/d(end state) of every chunk, transposed
   uint16_t* dd;           // [B*T][Hv][V]   bf16: dL/dd
 };
-
-// ------------------------------------------------------ reverse chain ----
-template <int K>
-struct RevIn {
-  static constexpr int KB = K / 32;
-  u16x8 kf[KB], qf[KB];   // K / Q rows 16w + r16 (A operand of K dS'; staged for K^T, Q^T)
-  u16x8 tf[2][2];         // Tb^T rows [k-block][hi, lo]
-  u16x8 pf[2];            // P^T rows [k-block]
-  u16x8 dof[2];           // dO[32 kb + 8 grp + i][16 vt + r16], i = 0..7 (B operand)
-  float G;                // G of row `lane`
-};
-
-struct RevCtx {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* dO;
-  BwdWs ws;
-  int s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane;
-  int kq_off;     // row 16w + r16, columns 8grp.. of a K / Q row (bytes)
-};
-
-template <int K>
-__device__ __forceinline__ void rev_load_a(RevIn<K>& in, const RevCtx& c, int ci) {
-  const int t0 = c.s + (ci - c.c_begin) * kChunk;
-  const int L = min(kChunk, c.e - t0);
-  const size_t row0 = (size_t)t0 * c.Hqk + c.hq;
-  const int bytes = L * c.Hqk * K * 2;
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(c.k + row0 * K), 0, bytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(c.q + row0 * K), 0, bytes, kBufferFlags);
-#pragma unroll
-  for (int b = 0; b < RevIn<K>::KB; ++b) {
-    in.kf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, c.kq_off + 64 * b, 0, 0));
-    in.qf[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, c.kq_off + 64 * b, 0, 0));
-  }
-}
-
-template <int K>
-__device__ __forceinline__ void rev_load_b(RevIn<K>& in, const RevCtx& c, int ci) {
-  const size_t base = ((size_t)ci * c.Hv + c.h) * 4 + c.w;
-  const u16x8* tb = c.ws.f.ttfrag + base * 256;
-  const u16x8* pb = c.ws.f.ptfrag + base * 128;
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    in.tf[b][0] = tb[128 * b + c.lane];
-    in.tf[b][1] = tb[128 * b + 64 + c.lane];
-    in.pf[b] = pb[64 * b + c.lane];
-  }
-}
-
-template <int K>
-__device__ __forceinline__ void rev_load_c(RevIn<K>& in, const RevCtx& c, int ci) {
-  const int t0 = c.s + (ci - c.c_begin) * kChunk;
-  const int L = min(kChunk, c.e - t0);
-  const int rowb = c.Hv * c.V * 2;
-  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(c.dO + ((size_t)t0 * c.Hv + c.h) * c.V + 16 * c.vt), 0,
-      (L - 1) * rowb + 32, kBufferFlags);
-  const int grp = c.lane / 16, r16 = c.lane % 16;
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      in.dof[kb][i] = __builtin_amdgcn_raw_buffer_load_b16(
-          rd, (32 * kb + 8 * grp + i) * rowb + 2 * r16, 0, 0);
-  }
-  in.G = c.ws.f.gate[((size_t)ci * c.Hv + c.h) * 64 + c.lane];
-}
-
-template <int K>
-__global__ __launch_bounds__(256) void chunk_rev_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ dO, const float* dht, float* dh0,
-    const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
-    float scale, BwdWs ws) {
-  constexpr int KB = K / 32;
-  constexpr int RT = K / 64;     // 16-row state tiles per wave
-  constexpr int LDS_ = K + 8;
-  constexpr int LDY = 72;
-  static_assert(KB % 2 == 0, "K dS' uses two accumulators per hi/lo part");
-  __shared__ __attribute__((aligned(16))) uint16_t DsT[2][16][LDS_];
-  __shared__ __attribute__((aligned(16))) uint16_t YsT[2][16][LDY];
-  __shared__ __attribute__((aligned(16))) uint16_t ZsT[2][16][LDY];
-  __shared__ __attribute__((aligned(16))) uint16_t Kl[64][LDS_];
-  __shared__ __attribute__((aligned(16))) uint16_t Ql[64][LDS_];
-  __shared__ __attribute__((aligned(16))) float Egw[4][64];   // wave-private e^G
-
-  const int NVT = V / 16;
-  // blockIdx -> (sequence, v-head, V tile) dealt over the XCDs as the
-  // forward chain does (a qk-head group stays on one XCD)
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  const int unit = NVT * (Hv / Hqk);
-  if (nb % (8 * unit) == 0) {
-    const int i = bid >> 3;
-    bid = ((i / unit) * 8 + (bid & 7)) * unit + i % unit;
-  } else if ((nb & 7) == 0) {
-    bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  }
-  const int vt = bid % NVT;
-  const int h = (bid / NVT) % Hv;
-  const int n = bid / NVT / Hv;
-  const int hq = h / (Hv / Hqk);
-
-  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
-  const int r16 = lane % 16, grp = lane / 16;
-
-  int s, e;
-  seq_bounds(cu, n, T, total, s, e);
-  const int nct = (T + kChunk - 1) / kChunk;
-  const int c_begin = cu ? ws.f.off[n] : n * nct, c_end = cu ? ws.f.off[n + 1] : (n + 1) * nct;
-  const RevCtx ctx{q, k, dO, ws, s, e, c_begin, h, hq, Hqk, Hv, V, vt, w, lane,
-                   ((16 * w + r16) * Hqk * K + 8 * grp) * 2};
-
-  // dS' slice: rows w*16*RT + 16*tt + 4*grp + r, column 16*vt + r16
-  const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
-  f32x4 Dr[RT];
-#pragma unroll
-  for (int tt = 0; tt < RT; ++tt) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
-      Dr[tt][r] = dht ? dht[tile + (size_t)kd * V] : 0.f;
-    }
-  }
-  auto publish = [&]() {
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-      u16x4 hi4, lo4;
-      split_bf4(Dr[tt], hi4, lo4);
-      const int kd0 = w * 16 * RT + 16 * tt + 4 * grp;
-      *reinterpret_cast<u16x4*>(&DsT[0][r16][kd0]) = hi4;
-      *reinterpret_cast<u16x4*>(&DsT[1][r16][kd0]) = lo4;
-    }
-  };
-  publish();
-  __syncthreads();
-
-  auto step = [&](RevIn<K>& cur, RevIn<K>& nxt, int ci, int cn, int cn2) {
-    const int t0 = s + (ci - c_begin) * kChunk;
-    const int L = min(kChunk, e - t0);
-    // this thread's 16 bytes of the published bf16 dS' (DsT[0] = dS'^T of
-    // this V tile), stored after the step's last prefetch
-    u16x8 dsv = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (tid < 16 * K / 8)
-      dsv = *reinterpret_cast<const u16x8*>(&DsT[0][tid / (K / 8)][8 * (tid % (K / 8))]);
-    rev_load_a<K>(nxt, ctx, cn);
-    const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.G), L - 1));
-    const float egx = __expf(cur.G), decx = __expf(GL - cur.G);
-    f32x4 eg, dec;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int src = (16 * w + 4 * grp + r) * 4;
-      eg[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(egx)));
-      dec[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(decx)));
-    }
-    const float egl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(egx), L - 1));
-    Egw[w][lane] = egx;
-#pragma unroll
-    for (int b = 0; b < KB; ++b) {
-      *reinterpret_cast<u16x8*>(&Kl[16 * w + r16][32 * b + 8 * grp]) = cur.kf[b];
-      *reinterpret_cast<u16x8*>(&Ql[16 * w + r16][32 * b + 8 * grp]) = cur.qf[b];
-    }
-    // X = K dS' (hi + lo)
-    f32x4 xa = zero4(), xb = zero4(), xc = zero4(), xd = zero4();
-#pragma unroll
-    for (int b = 0; b < KB; b += 2) {
-      const u16x8 sh0 = *reinterpret_cast<const u16x8*>(&DsT[0][r16][32 * b + 8 * grp]);
-      const u16x8 sl0 = *reinterpret_cast<const u16x8*>(&DsT[1][r16][32 * b + 8 * grp]);
-      const u16x8 sh1 = *reinterpret_cast<const u16x8*>(&DsT[0][r16][32 * b + 32 + 8 * grp]);
-      const u16x8 sl1 = *reinterpret_cast<const u16x8*>(&DsT[1][r16][32 * b + 32 + 8 * grp]);
-      xa = mfma16(cur.kf[b], sh0, xa);
-      xb = mfma16(cur.kf[b + 1], sh1, xb);
-      xc = mfma16(cur.kf[b], sl0, xc);
-      xd = mfma16(cur.kf[b + 1], sl1, xd);
-    }
-    u16x4 ddsave;
-    // P^T dO (bf16 operands, exact products)
-    const f32x4 pd = mfma16(cur.pf[1], cur.dof[1], mfma16(cur.pf[0], cur.dof[0], zero4()));
-    {
-      const f32x4 X = (xa + xb) + (xc + xd);
-      const f32x4 y = dec * X + pd;
-      u16x4 yh, yl;
-      split_bf4(y, yh, yl);
-      *reinterpret_cast<u16x4*>(&YsT[0][r16][16 * w + 4 * grp]) = yh;
-      *reinterpret_cast<u16x4*>(&YsT[1][r16][16 * w + 4 * grp]) = yl;
-      ddsave = yh;
-    }
-    __syncthreads();
-    rev_load_b<K>(nxt, ctx, cn);
-
-    // K^T and Q^T fragments of the update (rows of this wave's state tiles)
-    u16x8 ka[RT][2], qa[RT][2];
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-      const int kd0 = w * 16 * RT + 16 * tt;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        ka[tt][b] = lds_colfrag(&Kl[0][0], LDS_, 32 * b, kd0, lane);
-        qa[tt][b] = lds_colfrag(&Ql[0][0], LDS_, 32 * b, kd0, lane);
-      }
-    }
-    // Z = Tb^T dd (three hi/lo terms)
-    {
-      f32x4 va = zero4(), vb = zero4(), vc = zero4();
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const u16x8 yh = *reinterpret_cast<const u16x8*>(&YsT[0][r16][32 * b + 8 * grp]);
-        const u16x8 yl = *reinterpret_cast<const u16x8*>(&YsT[1][r16][32 * b + 8 * grp]);
-        va = mfma16(cur.tf[b][0], yh, va);
-        vb = mfma16(cur.tf[b][0], yl, vb);
-        vc = mfma16(cur.tf[b][1], yh, vc);
-      }
-      const f32x4 z = -(eg * (va + (vb + vc)));
-      u16x4 zh, zl;
-      split_bf4(z, zh, zl);
-      *reinterpret_cast<u16x4*>(&ZsT[0][r16][16 * w + 4 * grp]) = zh;
-      *reinterpret_cast<u16x4*>(&ZsT[1][r16][16 * w + 4 * grp]) = zl;
-    }
-    // B operand of the Q^T term: c' e^G_j dO[j], j = 32 kb + 8 grp + i (hi + lo)
-    u16x8 oh[2], ol[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const f32x4 e0 = *reinterpret_cast<const f32x4*>(&Egw[w][32 * kb + 8 * grp]);
-      const f32x4 e1 = *reinterpret_cast<const f32x4*>(&Egw[w][32 * kb + 8 * grp + 4]);
-      f32x4 x0, x1;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x0[i] = scale * e0[i] * bf2f(cur.dof[kb][i]);
-        x1[i] = scale * e1[i] * bf2f(cur.dof[kb][4 + i]);
-      }
-      u16x4 h0v, l0v, h1v, l1v;
-      split_bf4(x0, h0v, l0v);
-      split_bf4(x1, h1v, l1v);
-      oh[kb] = u16x8{h0v[0], h0v[1], h0v[2], h0v[3], h1v[0], h1v[1], h1v[2], h1v[3]};
-      ol[kb] = u16x8{l0v[0], l0v[1], l0v[2], l0v[3], l1v[0], l1v[1], l1v[2], l1v[3]};
-    }
-    __syncthreads();
-    // dO and G two chunks ahead, into this step's own buffer (last read
-    // before the second barrier): the first operands a step waits for
-    rev_load_c<K>(cur, ctx, cn2);
-    // stores after the step's last prefetch: vector memory operations retire
-    // in issue order, so a store ahead of a prefetch delays that prefetch's wait
-    {
-      if (tid < 16 * K / 8)
-        *reinterpret_cast<u16x8*>(ws.dse + (((size_t)ci * Hv + h) * V + 16 * vt + tid / (K / 8)) * K +
-                                  8 * (tid % (K / 8))) = dsv;
-      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
-          ws.dd + (size_t)t0 * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        __builtin_amdgcn_raw_buffer_store_b16(
-            ddsave[r], dr, (((16 * w + 4 * grp + r) * Hv + h) * V + 16 * vt + r16) * 2, 0, 0);
-    }
-
-    // dS = e^G_L dS' + K^T (-e^G Z) + Q^T (c' e^G dO)
-    {
-      u16x8 zh[2], zl[2];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        zh[b] = *reinterpret_cast<const u16x8*>(&ZsT[0][r16][32 * b + 8 * grp]);
-        zl[b] = *reinterpret_cast<const u16x8*>(&ZsT[1][r16][32 * b + 8 * grp]);
-      }
-#pragma unroll
-      for (int tt = 0; tt < RT; ++tt) {
-        f32x4 a0 = Dr[tt] * egl, a1 = zero4(), a2 = zero4(), a3 = zero4();
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          a0 = mfma16(ka[tt][b], zh[b], a0);
-          a1 = mfma16(ka[tt][b], zl[b], a1);
-          a2 = mfma16(qa[tt][b], oh[b], a2);
-          a3 = mfma16(qa[tt][b], ol[b], a3);
-        }
-        Dr[tt] = (a0 + a1) + (a2 + a3);
-      }
-    }
-    publish();
-    __syncthreads();
-  };
-
-  RevIn<K> bufA, bufB;
-  if (c_begin < c_end) {
-    rev_load_a<K>(bufA, ctx, c_end - 1);
-    rev_load_b<K>(bufA, ctx, c_end - 1);
-    rev_load_c<K>(bufA, ctx, c_end - 1);
-    rev_load_c<K>(bufB, ctx, max(c_end - 2, c_begin));
-  }
-  // Nothing outstanding on entry, and pairs of steps with an odd last chunk
-  // outside the loop, so the wait counts at the loop head cover only the
-  // prefetch the next step needs (see the forward chain).
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  int ci = c_end - 1;
-  for (; ci - 1 >= c_begin; ci -= 2) {
-    step(bufA, bufB, ci, ci - 1, max(ci - 2, c_begin));
-    step(bufB, bufA, ci - 1, max(ci - 2, c_begin), max(ci - 3, c_begin));
-  }
-  if (ci >= c_begin) step(bufA, bufB, ci, ci, ci);
-
-  if (dh0) {
-#pragma unroll
-    for (int tt = 0; tt < RT; ++tt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kd = w * 16 * RT + 16 * tt + 4 * grp + r;
-        dh0[tile + (size_t)kd * V] = Dr[tt][r];
-      }
-    }
-  }
-}
-
-}  // namespace gdn
-
-namespace gdn {
 
 // --------------------------------------------------- gradient kernel ----
 // One workgroup of 8 waves per (chunk, qk-head).  Wave w8 owns row tile
@@ -1028,8 +714,7 @@ static void launch_bwd_kernels(const uint16_t* q, const uint16_t* k, const uint1
   ws.dse = reinterpret_cast<uint16_t*>(wsb + p.dse);
   ws.dd = reinterpret_cast<uint16_t*>(wsb + p.dd);
   const int total = B * T;
-  hipLaunchKernelGGL((chunk_rev_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, qn, kn,
-                     dO, dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  launch_rev_sw<K>(kn, dO, dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws.f, ws.dse, ws.dd, st);
   if (p.ncmax > 0)
     hipLaunchKernelGGL((chunk_grad_kernel<K, V>), dim3((unsigned)p.ncmax, Hqk), dim3(kGradThreads), 0,
                        st, qn, kn, q, k, v, dO, beta, cu, N, T, total, Hqk, Hv, scale,

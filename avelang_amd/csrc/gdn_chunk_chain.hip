@@ -37,42 +37,6 @@
 
 namespace gdn {
 
-// rho of tile row 16 T + m (m < 16)
-__device__ __forceinline__ int rho_row(int T, int m) {
-  return 32 * (T >> 1) + 8 * (m >> 2) + 4 * (T & 1) + (m & 3);
-}
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ u16x8 cat8(u16x4 a, u16x4 b) {
-  return u16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
-// Tb fragment slot of (row tile ti, k-block b): row tiles 0 and 1 have no
-// k-block 1 (Tb is lower triangular), so six slots per hi / lo part.
-__device__ __forceinline__ constexpr int tb_slot(int ti, int b) { return b == 0 ? ti : 2 + ti; }
-
-// s_waitcnt immediate (gfx9 encoding) that waits until at most n
-// vector-memory operations are outstanding, and for nothing else.
-__device__ __forceinline__ constexpr int vmcnt_imm(int n) {
-  return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14);
-}
-
-// Staged K rows: row stride 2K + 16 bytes and 64 more bytes after every 16
-// rows.  The column-fragment reads of the state wave (16 rows rho(16 ti +
-// m), one 16-byte piece) then fall on distinct banks, and every K read is a
-// per-lane base plus a compile-time offset.
-template <int K>
-struct KLayout {
-  static constexpr int RS = 2 * K + 16;            // row stride (bytes)
-  static constexpr int GP = 64;                    // extra bytes per 16 rows
-  static constexpr int GU = (16 * RS + GP) / 16;   // 16-byte units per 16 rows
-  static constexpr int UNITS = 4 * GU;             // units of the 64 rows
-  static constexpr int LOADS = (UNITS + 63) / 64;  // 1 KiB direct-to-LDS loads
-  static constexpr int BYTES = LOADS * 1024;       // buffer size
-  __device__ static constexpr int row(int r) { return r * RS + (r >> 4) * GP; }
-};
-
 // SAVE: store the state at every chunk start (ws.hs, bf16, transposed) and
 // the per-token delta vnew (ws.dl, bf16) for the backward.  OUT: write o and
 // ht.  Forward <K, false, true>, the backward's recomputation <K, true,

@@ -1,0 +1,485 @@
+// Reverse chain of the chunked backward, state-wave form (gfx950).
+//
+// Per chunk, from the last to the first (dS' = dL/d(state at the chunk's
+// end), c' = scale; the backward's derivation is in gdn_chunk_bwd.hip):
+//     dd = P^T dO + e^(G_L - G) (K dS'),   Z = Tb^T dd,
+//     dS = e^G_L dS' - K^T (e^G Z) + Q^T (c' e^G dO)
+// and dS becomes the previous chunk's dS'.  Stored for the gradient kernel:
+// dS' of every chunk (bf16, transposed) and dd (bf16, token-major); dh0.
+//
+// The layout of the forward chain (gdn_chunk_chain.hip), with two helper
+// waves in place of its output wave:
+//
+//   wave 0, the state wave, holds every key row of the tile's dS' in VGPRs
+//   (rho row order) and runs the dS'-dependent products alone: K dS' (hi +
+//   lo), Tb^T dd (three hi / lo terms), K^T U (hi + lo), every operand from
+//   LDS and every result tile the next product's B operand where it stands.
+//   The terms that do not depend on dS' -- P^T dO and Q^T (c' e^G dO) -- it
+//   reads as fp32 tiles in its own layout.
+//
+//   wave 1, the stage wave, loads the K rows and Tb^T fragments of the chunk
+//   two steps ahead straight into LDS (buffer_load ... lds).
+//
+//   waves 2 and 3, the helper waves, form the next step's gate factors and
+//   P^T dO (wave 2) and Q^T (c' e^G dO) (wave 3) from the prep's P^T and
+//   Q^T fragments and dO, write them into LDS, and store the previous
+//   step's dS' and dd (wave 2).
+//
+// Step j works on chunk nc - 1 - j of the sequence.
+#include <type_traits>
+
+#include "gdn_chunk.h"
+
+namespace gdn {
+
+template <int K>
+__global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ dO, const float* dht,
+    float* dh0, const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
+    float scale, ChunkWs ws, uint16_t* __restrict__ dse, uint16_t* __restrict__ ddo) {
+  constexpr int KB = K / 32;   // k-blocks over the key index
+  constexpr int ST = K / 16;   // 16-row state tiles
+  using KL = KLayout<K>;
+  // stage buffers (step j in buffer j % 3): K rows, Tb^T fragments by rho row
+  __shared__ __attribute__((aligned(16))) unsigned char Kst[3][KL::BYTES];
+  __shared__ __attribute__((aligned(16))) u16x8 Tst[3][6][2][64];
+  // helper -> state: e^G and e^(G_last - G) by token, e^G_last, P^T dO
+  // (token tiles in the state wave's layout) and Q^T (c' e^G dO) (state tiles)
+  __shared__ __attribute__((aligned(16))) float Gst[3][2][64];
+  __shared__ float Egl[3];
+  __shared__ __attribute__((aligned(16))) f32x4 Pst[3][4][64];
+  __shared__ __attribute__((aligned(16))) f32x4 Qst[3][ST][64];
+  // state -> helper: dS' hi B fragments at the step's start, dd (bf16) as B
+  // fragments
+  __shared__ __attribute__((aligned(16))) u16x8 Sx[3][KB][64];
+  __shared__ __attribute__((aligned(16))) u16x8 Vx[3][2][64];
+
+  const int NVT = V / 16;
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  const int unit = NVT * (Hv / Hqk);
+  if (nb % (8 * unit) == 0) {
+    const int i = bid >> 3;
+    bid = ((i / unit) * 8 + (bid & 7)) * unit + i % unit;
+  } else if ((nb & 7) == 0) {
+    bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  }
+  const int vt = bid % NVT;
+  const int h = (bid / NVT) % Hv;
+  const int n = bid / NVT / Hv;
+  const int hq = h / (Hv / Hqk);
+
+  const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int r16 = lane % 16, grp = lane / 16;
+
+  int s, e;
+  seq_bounds(cu, n, T, total, s, e);
+  const int nct = (T + kChunk - 1) / kChunk;
+  const int c_begin = cu ? ws.off[n] : n * nct;
+  const int nc = (cu ? ws.off[n + 1] : (n + 1) * nct) - c_begin;
+
+  if (w == 0) {
+    // ------------------------------------------------------ state wave ----
+    const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
+    f32x4 S[ST];
+    if (dht) {
+#pragma unroll
+      for (int t = 0; t < ST; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[t][r] = dht[tile + (size_t)rho_row(t, 4 * grp + r) * V];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < ST; ++t) S[t] = zero4();
+    }
+    __syncthreads();   // stage buffer 0 and the helper's first tiles are in
+
+    const int m4 = r16 >> 2, q4 = r16 & 3;
+    int ka_off[4];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) ka_off[ti] = KL::row(rho_row(ti, r16)) + 16 * grp;
+    const int tr_lo = KL::row(8 * grp + m4) + 16 * q4;
+    const int tr_hi = KL::row(8 * grp + 4 + m4) + 16 * q4;
+
+    auto step = [&](auto b3c) {
+      constexpr int b3 = decltype(b3c)::value;
+      const unsigned char* Kb = Kst[b3];
+      u16x8 ka[KB][4], ta[6][2];
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+          ka[b][ti] = *reinterpret_cast<const u16x8*>(Kb + ka_off[ti] + 64 * b);
+      }
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        ta[i][0] = Tst[b3][i][0][lane];
+        ta[i][1] = Tst[b3][i][1][lane];
+      }
+      f32x4 eg[4], dc[4], pd[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int r0 = 32 * (ti >> 1) + 8 * grp + 4 * (ti & 1);
+        eg[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][0][r0]);
+        dc[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][1][r0]);
+        pd[ti] = Pst[b3][ti][lane];
+      }
+      const float egl = Egl[b3];
+
+      // X = K dS' on the rho-ordered token tiles (dS' hi also to the helper)
+      f32x4 X[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) X[ti] = zero4();
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        u16x4 h0v, l0v, h1v, l1v;
+        split_bf4(S[2 * b], h0v, l0v);
+        split_bf4(S[2 * b + 1], h1v, l1v);
+        const u16x8 sh = cat8(h0v, h1v), sl = cat8(l0v, l1v);
+        Sx[b3][b][lane] = sh;
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sh, X[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sl, X[ti]);
+      }
+      // dd = P^T dO + e^(G_L - G) X on token tiles 2b, 2b + 1 (hi, lo B
+      // fragments of k-block b of Tb^T dd; hi also stored as dd)
+      auto ddsplit = [&](int b, u16x8& yh, u16x8& yl) {
+        u16x4 hh0, ll0, hh1, ll1;
+        split_bf4(pd[2 * b] + dc[2 * b] * X[2 * b], hh0, ll0);
+        split_bf4(pd[2 * b + 1] + dc[2 * b + 1] * X[2 * b + 1], hh1, ll1);
+        yh = cat8(hh0, hh1);
+        yl = cat8(ll0, ll1);
+        Vx[b3][b][lane] = yh;
+      };
+      // Z = Tb^T dd: Tb^T is upper triangular, so token tiles 2 and 3 have
+      // no k-block 0; k-block 1 first, where every tile has a term
+      f32x4 z[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) z[ti] = zero4();
+      {
+        u16x8 yh, yl;
+        ddsplit(1, yh, yl);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 1)][0], yh, z[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 1)][0], yl, z[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 1)][1], yh, z[ti]);
+      }
+      u16x8 kt[2][ST];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int t = 0; t < ST; ++t) {
+          const int imm = KL::row(32 * b) + 64 * (t >> 1) + 8 * (t & 1);
+          const u16x4 lo4 = lds_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_lo + imm));
+          const u16x4 hi4 = lds_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_hi + imm));
+          kt[b][t] = cat8(lo4, hi4);
+        }
+      }
+      {
+        u16x8 yh, yl;
+        ddsplit(0, yh, yl);
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 0)][0], yh, z[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 0)][0], yl, z[ti]);
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 0)][1], yh, z[ti]);
+      }
+      // dS = e^G_L dS' + Q^T (c' e^G dO) + K^T U,  U = -e^G Z, block by block
+#pragma unroll
+      for (int t = 0; t < ST; ++t) S[t] = S[t] * egl + Qst[b3][t][lane];
+#pragma unroll
+      for (int b = 1; b >= 0; --b) {
+        u16x4 hh0, ll0, hh1, ll1;
+        split_bf4(-(eg[2 * b] * z[2 * b]), hh0, ll0);
+        split_bf4(-(eg[2 * b + 1] * z[2 * b + 1]), hh1, ll1);
+        const u16x8 uh = cat8(hh0, hh1), ul = cat8(ll0, ll1);
+#pragma unroll
+        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], uh, S[t]);
+#pragma unroll
+        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], ul, S[t]);
+      }
+      __syncthreads();   // step j's outputs published; stage buffer j % 3 free
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    int j = 0;
+    for (; j + 2 < nc; j += 3) {
+      step(I0{});
+      step(I1{});
+      step(I2{});
+    }
+    if (j < nc) step(I0{});
+    if (j + 1 < nc) step(I1{});
+    if (dh0) {
+#pragma unroll
+      for (int t = 0; t < ST; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dh0[tile + (size_t)rho_row(t, 4 * grp + r) * V] = S[t][r];
+      }
+    }
+  } else if (w == 1) {
+    // ------------------------------------------------------ stage wave ----
+    // As in the forward chain: step j + 2's K rows and Tb^T fragments
+    // straight to LDS during step j, bare barriers, explicit waits.
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    constexpr int P = K / 8;
+    constexpr int kKT = KL::LOADS + 12;
+    const int rowq = Hqk * K * 2;
+    auto issue_kt = [&](int j, int jb) {
+      const int jc = nc - 1 - j;
+      const int ci = c_begin + jc, buf = jb % 3;
+      const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(k + ((size_t)t0 * Hqk + hq) * K), 0, L * rowq, kBufferFlags);
+#pragma unroll
+      for (int i = 0; i < KL::LOADS; ++i) {
+        const int p = 64 * i + lane;
+        const int g16 = p / KL::GU, rem = p % KL::GU;
+        const int row = 16 * g16 + rem / (KL::RS / 16), piece = rem % (KL::RS / 16);
+        const bool data = rem < 16 * (KL::RS / 16) && piece < P && p < KL::UNITS;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(Kst[buf] + 1024 * i), 16,
+                                                 data ? row * rowq + 16 * piece : 0x7ffffff0,
+                                                 0, 0, 0);
+      }
+      // Tb^T fragments gathered by rho row (token tiles 2, 3 have no k-block 0)
+      const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+          ws.ttfrag + ((size_t)ci * Hv + h) * 4 * 256, 0, 4 * 256 * 16, kBufferFlags);
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int row = rho_row(ti, r16);
+        const int src = (row >> 4) * 256 + (row & 15) + 16 * grp;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          if (b == 0 && ti >= 2) continue;
+#pragma unroll
+          for (int hl = 0; hl < 2; ++hl)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr)&Tst[buf][tb_slot(ti, b)][hl][0],
+                                                     16, (src + 128 * b + 64 * hl) * 16, 0, 0, 0);
+        }
+      }
+    };
+    auto barrier = [] {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    };
+    if (nc > 0) {
+      issue_kt(0, 0);
+      issue_kt(min(1, nc - 1), 1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // step 0's
+    }
+    barrier();
+    for (int j = 0; j < nc; ++j) {
+      issue_kt(min(j + 2, nc - 1), j + 2);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // step j+1's
+      barrier();
+    }
+  } else {
+    // ---------------------------------------------------- helper waves ----
+    // Wave 2 forms step j+1's gate factors and P^T dO into LDS and stores
+    // step j-1's dS' and dd; wave 3 forms step j+1's Q^T (c' e^G dO).  Each
+    // uses the register set it loaded two steps before and then loads step
+    // j+3's operands into it.  Every step issues the same loads and stores,
+    // so each wait names an exact count.
+    // one code path per role (a compile-time flag), so that no join of the
+    // two roles' loads blurs the compiler's wait counts
+    auto helper = [&](auto qwc) {
+      constexpr bool qwave = decltype(qwc)::value;
+      constexpr int kStep = qwave ? 2 * ST + 16 + 1 : 6 + 16 + 1 + KB + 2;
+      struct Regs {
+        u16x8 pt[6];        // P^T fragments (rho rows) by tb_slot (wave 2)
+        u16x8 qt[ST][2];    // Q^T fragments (rho key rows) by token k-block (wave 3)
+        u16x8 dof[2];       // dO[32 kb + 8 grp + i][16 vt + r16] (B operand)
+        float G;            // G of token `lane`
+      };
+      Regs rA, rB;
+      auto load = [&](Regs& r, int j) {
+        const int jc = nc - 1 - j;
+        const int ci = c_begin + jc;
+        const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
+        if constexpr (qwave) {
+          const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+              ws.qtfrag + ((size_t)ci * Hqk + hq) * ST * 128, 0, ST * 128 * 16, kBufferFlags);
+  #pragma unroll
+          for (int t = 0; t < ST; ++t) {
+            const int row = rho_row(t, r16);
+            const int src = (row >> 4) * 128 + (row & 15) + 16 * grp;
+  #pragma unroll
+            for (int b = 0; b < 2; ++b)
+              r.qt[t][b] = __builtin_bit_cast(
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, (src + 64 * b) * 16, 0, 0));
+          }
+        } else {
+          const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+              ws.ptfrag + ((size_t)ci * Hv + h) * 4 * 128, 0, 4 * 128 * 16, kBufferFlags);
+  #pragma unroll
+          for (int ti = 0; ti < 4; ++ti) {
+            const int row = rho_row(ti, r16);
+            const int src = (row >> 4) * 128 + (row & 15) + 16 * grp;
+  #pragma unroll
+            for (int b = 0; b < 2; ++b) {
+              if (b == 0 && ti >= 2) continue;
+              r.pt[tb_slot(ti, b)] = __builtin_bit_cast(
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (src + 64 * b) * 16, 0, 0));
+            }
+          }
+        }
+        const int rowb = Hv * V * 2;
+        const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V + 16 * vt), 0,
+            (L - 1) * rowb + 32, kBufferFlags);
+  #pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+  #pragma unroll
+          for (int i = 0; i < 8; ++i)
+            r.dof[kb][i] = __builtin_amdgcn_raw_buffer_load_b16(
+                rd, (32 * kb + 8 * grp + i) * rowb + 2 * r16, 0, 0);
+        }
+        const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+            ws.gate + ((size_t)ci * Hv + h) * 64, 0, 256, kBufferFlags);
+        r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
+      };
+      // step j's gate factors and P^T dO (wave 2) or Q^T (c' e^G dO) (wave 3)
+      // into buffer j % 3
+      auto publish = [&](const Regs& r, int j) {
+        const int buf = j % 3;
+        const float eg = __expf(r.G);
+        if constexpr (qwave) {
+          // c' e^G dO for this lane's k-slots (tokens 32 kb + 8 grp + i), hi + lo
+          u16x8 oh[2], ol[2];
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            f32x4 x0, x1;
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int src = 4 * (32 * kb + 8 * grp + i);
+              const float e0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(eg)));
+              const float e1 = __int_as_float(__builtin_amdgcn_ds_bpermute(src + 16, __float_as_int(eg)));
+              x0[i] = scale * e0 * bf2f(r.dof[kb][i]);
+              x1[i] = scale * e1 * bf2f(r.dof[kb][4 + i]);
+            }
+            u16x4 h0v, l0v, h1v, l1v;
+            split_bf4(x0, h0v, l0v);
+            split_bf4(x1, h1v, l1v);
+            oh[kb] = cat8(h0v, h1v);
+            ol[kb] = cat8(l0v, l1v);
+          }
+  #pragma unroll
+          for (int t = 0; t < ST; ++t) {
+            f32x4 a = zero4(), b = zero4();
+  #pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+              a = mfma16(r.qt[t][kb], oh[kb], a);
+              b = mfma16(r.qt[t][kb], ol[kb], b);
+            }
+            Qst[buf][t][lane] = a + b;
+          }
+        } else {
+          const int jc = nc - 1 - j;
+          const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
+          const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
+          Gst[buf][0][lane] = eg;
+          Gst[buf][1][lane] = __expf(GL - r.G);
+          if (lane == L - 1) Egl[buf] = eg;
+  #pragma unroll
+          for (int ti = 0; ti < 4; ++ti) {
+            f32x4 pd = mfma16(r.pt[tb_slot(ti, 1)], r.dof[1], zero4());
+            if (ti < 2) pd = mfma16(r.pt[tb_slot(ti, 0)], r.dof[0], pd);
+            Pst[buf][ti][lane] = pd;
+          }
+        }
+      };
+      typedef unsigned int u32x4l __attribute__((ext_vector_type(4)));
+      // step j's dS' (dse[chunk][v-head] = dS'^T, [V][K], bf16) and dd
+      // (token-major), wave 2; live = false (no step yet) stores to empty
+      // resources
+      auto save = [&](int j, bool live) {
+        if constexpr (qwave) return;
+        const int jc = nc - 1 - j;
+        const int t0 = s + jc * kChunk, L = live ? min(kChunk, e - t0) : 0;
+        const int b3 = j % 3;
+        const size_t ci = live ? (size_t)(c_begin + jc) : 0;
+        u16x8 sh[KB];
+        if (live) {
+  #pragma unroll
+          for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][b][lane];
+        }
+        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+            dse + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
+  #pragma unroll
+        for (int b = 0; b < KB; ++b)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, sh[b]), hr,
+                                                 ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
+        // lane t gathers token row t of dd from the fragments in LDS (element
+        // t % 8 of fragment lane 16 ((t / 8) % 4) + n of k-block t / 32)
+        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+            ddo + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+        u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
+        if (live) {
+          const uint16_t* src =
+              reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
+              (lane & 7);
+  #pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            d0[c] = src[8 * c];
+            d1[c] = src[8 * (c + 8)];
+          }
+        }
+        const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d0), dr, drow, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d1), dr, drow + 16, 0, 0);
+      };
+      if (nc > 0) {
+        load(rA, 0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        publish(rA, 0);
+        load(rB, min(1, nc - 1));
+        save(0, false);                  // the stores a step issues, dropped
+        load(rA, min(2, nc - 1));
+      }
+      __syncthreads();
+      // step j works on register set (j + 1) % 2
+      auto hstep = [&](int j, Regs& r) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kStep));   // step j+1's operands
+        if (j + 1 < nc) publish(r, j + 1);
+        save(j - 1, j >= 1);
+        load(r, min(j + 3, nc - 1));
+        __syncthreads();
+      };
+      int j = 0;
+      for (; j + 1 < nc; j += 2) {
+        hstep(j, rB);
+        hstep(j + 1, rA);
+      }
+      if (j < nc) hstep(j, rB);
+      if (nc > 0) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        save(nc - 1, true);
+      }
+    };
+    if (w == 3) helper(std::true_type{});
+    else helper(std::false_type{});
+  }
+}
+
+template <int K>
+void launch_rev_sw(const uint16_t* k, const uint16_t* dO, const float* dht, float* dh0,
+                   const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
+                   float scale, const ChunkWs& ws, uint16_t* dse, uint16_t* dd, hipStream_t st) {
+  hipLaunchKernelGGL((chunk_rev_sw_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, k, dO,
+                     dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws, dse, dd);
+}
+
+template void launch_rev_sw<64>(const uint16_t*, const uint16_t*, const float*, float*,
+                                const int32_t*, int, int, int, int, int, int, float,
+                                const ChunkWs&, uint16_t*, uint16_t*, hipStream_t);
+template void launch_rev_sw<128>(const uint16_t*, const uint16_t*, const float*, float*,
+                                 const int32_t*, int, int, int, int, int, int, float,
+                                 const ChunkWs&, uint16_t*, uint16_t*, hipStream_t);
+
+}  // namespace gdn

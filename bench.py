@@ -577,7 +577,7 @@ def pmc_summary(fetch_dir, write_dir, out_path):
         "decode": total(lambda k: "recurrent_kernel<128, 128" in k),
         "backward": total(lambda k: ("chunk_prep_kernel<128, true>" in k
                                      or "chunk_chain_sw_kernel<128, true, false>" in k
-                                     or "chunk_rev_kernel<128>" in k
+                                     or "chunk_rev_sw_kernel<128>" in k
                                      or "chunk_grad_kernel<128, 128>" in k)),
         "per_kernel": kern,
         "fetch_size_factor": round(ff, 4),
