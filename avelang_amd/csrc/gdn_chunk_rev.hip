@@ -305,11 +305,11 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         if constexpr (qwave) {
           const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
               ws.qtfrag + ((size_t)ci * Hqk + hq) * ST * 128, 0, ST * 128 * 16, kBufferFlags);
-  #pragma unroll
+#pragma unroll
           for (int t = 0; t < ST; ++t) {
             const int row = rho_row(t, r16);
             const int src = (row >> 4) * 128 + (row & 15) + 16 * grp;
-  #pragma unroll
+#pragma unroll
             for (int b = 0; b < 2; ++b)
               r.qt[t][b] = __builtin_bit_cast(
                   u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, (src + 64 * b) * 16, 0, 0));
@@ -317,11 +317,11 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         } else {
           const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
               ws.ptfrag + ((size_t)ci * Hv + h) * 4 * 128, 0, 4 * 128 * 16, kBufferFlags);
-  #pragma unroll
+#pragma unroll
           for (int ti = 0; ti < 4; ++ti) {
             const int row = rho_row(ti, r16);
             const int src = (row >> 4) * 128 + (row & 15) + 16 * grp;
-  #pragma unroll
+#pragma unroll
             for (int b = 0; b < 2; ++b) {
               if (b == 0 && ti >= 2) continue;
               r.pt[tb_slot(ti, b)] = __builtin_bit_cast(
@@ -333,9 +333,9 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V + 16 * vt), 0,
             (L - 1) * rowb + 32, kBufferFlags);
-  #pragma unroll
+#pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 8; ++i)
             r.dof[kb][i] = __builtin_amdgcn_raw_buffer_load_b16(
                 rd, (32 * kb + 8 * grp + i) * rowb + 2 * r16, 0, 0);
@@ -352,10 +352,10 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         if constexpr (qwave) {
           // c' e^G dO for this lane's k-slots (tokens 32 kb + 8 grp + i), hi + lo
           u16x8 oh[2], ol[2];
-  #pragma unroll
+#pragma unroll
           for (int kb = 0; kb < 2; ++kb) {
             f32x4 x0, x1;
-  #pragma unroll
+#pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int src = 4 * (32 * kb + 8 * grp + i);
               const float e0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(eg)));
@@ -369,10 +369,10 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
             oh[kb] = cat8(h0v, h1v);
             ol[kb] = cat8(l0v, l1v);
           }
-  #pragma unroll
+#pragma unroll
           for (int t = 0; t < ST; ++t) {
             f32x4 a = zero4(), b = zero4();
-  #pragma unroll
+#pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
               a = mfma16(r.qt[t][kb], oh[kb], a);
               b = mfma16(r.qt[t][kb], ol[kb], b);
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
           Gst[buf][0][lane] = eg;
           Gst[buf][1][lane] = __expf(GL - r.G);
           if (lane == L - 1) Egl[buf] = eg;
-  #pragma unroll
+#pragma unroll
           for (int ti = 0; ti < 4; ++ti) {
             f32x4 pd = mfma16(r.pt[tb_slot(ti, 1)], r.dof[1], zero4());
             if (ti < 2) pd = mfma16(r.pt[tb_slot(ti, 0)], r.dof[0], pd);
@@ -406,12 +406,12 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         const size_t ci = live ? (size_t)(c_begin + jc) : 0;
         u16x8 sh[KB];
         if (live) {
-  #pragma unroll
+#pragma unroll
           for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][b][lane];
         }
         const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
             dse + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < KB; ++b)
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, sh[b]), hr,
                                                  ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
           const uint16_t* src =
               reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
               (lane & 7);
-  #pragma unroll
+#pragma unroll
           for (int c = 0; c < 8; ++c) {
             d0[c] = src[8 * c];
             d1[c] = src[8 * (c + 8)];
