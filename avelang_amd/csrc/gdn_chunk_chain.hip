@@ -42,7 +42,7 @@ namespace gdn {
 // ht.  Forward <K, false, true>, the backward's recomputation <K, true,
 // false>, a training forward <K, true, true>.
 template <int K, bool SAVE, bool OUT>
-__global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
+__global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
@@ -327,7 +327,9 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
     // exact count.
     constexpr int kQP = OUT ? 4 * KB + 6 : 0;   // Q / P loads per chunk
     constexpr int kVG = 3;                      // V tile (2) + G (1)
-    constexpr int kSave = SAVE ? KB + 2 : 0;    // state and delta stores per chunk
+    // with both outputs, the saves go to a wave of their own (wave 3)
+    constexpr bool kSplit = SAVE && OUT;
+    constexpr int kSave = SAVE && !kSplit ? KB + 2 : 0;   // state and delta stores per chunk
     constexpr int kStep = (OUT ? 4 : 0) + kSave + kQP + kVG;   // stores + loads per step
     const int rowq = Hqk * K * 2;
     struct Regs {
@@ -394,13 +396,49 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
       Gst[buf][1][lane] = __expf(GL - r.G);
       if (lane == L - 1) Egl[buf] = eg;
     };
+    // SAVE: the chunk's start state (hs[chunk][v-head] = S^T, [V][K]: the
+    // state fragments as they stand, 16 bytes per k-block) and its deltas
+    // (dl, token-major); live = false stores to empty resources (dropped)
+    auto save_chunk = [&](int j, bool live) {
+      const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
+      const int b3 = j % 3;
+      u16x8 sh[KB];
+      if (live) {
+#pragma unroll
+        for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][b][lane];
+      }
+      const size_t ci = live ? (size_t)(c_begin + j) : 0;
+      const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+          ws.hs + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
+#pragma unroll
+      for (int b = 0; b < KB; ++b)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sh[b]), hr,
+                                               ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
+      // deltas: lane t gathers token row t (its 16 columns) from the vnew
+      // fragments in LDS -- element (t % 8) of fragment lane 16 ((t / 8) % 4)
+      // + n of k-block t / 32 -- and writes it with two 16-byte stores
+      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+          ws.dl + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+      u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
+      if (live) {
+        const uint16_t* src =
+            reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
+            (lane & 7);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          d0[c] = src[8 * c];
+          d1[c] = src[8 * (c + 8)];
+        }
+      }
+      const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr, drow, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), dr, drow + 16, 0, 0);
+    };
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     // o^T tiles of chunk j: lane (r16, grp) holds token row 16 ti + r16,
-    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile); SAVE: the
-    // chunk's start state (hs[chunk][v-head] = S^T, [V][K]: the state
-    // fragments as they stand, 16 bytes per k-block) and its deltas (dl,
-    // token-major).  With live = false (no chunk yet) every store goes to an
-    // empty resource and is dropped.
+    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile), and the
+    // chunk's saves when no save wave runs.  With live = false (no chunk
+    // yet) every store goes to an empty resource and is dropped.
     auto output = [&](const Regs& r, int j, bool live) {
       const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
       const int b3 = j % 3;
@@ -411,34 +449,7 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
         vx[0] = Vx[b3][0][lane];
         vx[1] = Vx[b3][1][lane];
       }
-      if constexpr (SAVE) {
-        const size_t ci = live ? (size_t)(c_begin + j) : 0;
-        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
-            ws.hs + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
-#pragma unroll
-        for (int b = 0; b < KB; ++b)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sh[b]), hr,
-                                                 ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
-        // deltas: lane t gathers token row t (its 16 columns) from the vnew
-        // fragments in LDS -- element (t % 8) of fragment lane 16 ((t / 8) % 4)
-        // + n of k-block t / 32 -- and writes it with two 16-byte stores
-        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
-            ws.dl + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-        u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
-        if (live) {
-          const uint16_t* src =
-              reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
-              (lane & 7);
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            d0[c] = src[8 * c];
-            d1[c] = src[8 * (c + 8)];
-          }
-        }
-        const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr, drow, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), dr, drow + 16, 0, 0);
-      }
+      if constexpr (SAVE && !kSplit) save_chunk(j, live);
       if constexpr (!OUT) return;
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
           o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
@@ -462,6 +473,16 @@ __global__ __launch_bounds__(192) void chunk_chain_sw_kernel(
             (((16 * ti + r16) * Hv + h) * V + 16 * vt + 4 * grp) * 2, 0, 0);
       }
     };
+    if (kSplit && w == 3) {
+      // the save wave: chunk j-1's state and deltas during step j
+      __syncthreads();
+      for (int j = 0; j < nc; ++j) {
+        if (j >= 1) save_chunk(j - 1, true);
+        __syncthreads();
+      }
+      if (nc > 0) save_chunk(nc - 1, true);
+      return;
+    }
     if (nc > 0) {
       load_vg(rA, 0);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -498,7 +519,7 @@ template <int K, bool SAVE, bool OUT>
 void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
                      float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
                      int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st) {
-  hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT>), dim3(N * Hv * (V / 16)), dim3(192), 0,
+  hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT>), dim3(N * Hv * (V / 16)), dim3(SAVE && OUT ? 256 : 192), 0,
                      st, q, k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
 }
 
