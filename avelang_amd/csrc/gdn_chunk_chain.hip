@@ -1,10 +1,11 @@
 // Forward chain of the chunked prefill, state-wave form (gfx950).
 //
-// One workgroup of three waves per (sequence, v-head, 16-column V tile),
-// sequential over the sequence's chunks of 64 tokens:
+// One workgroup per (sequence, v-head, 16-column V tile) -- or per two V
+// tiles when the chains fill the GPU twice over -- sequential over the
+// sequence's chunks of 64 tokens:
 //
-//   wave 0, the state wave, holds every key row of the tile's fp32 state in
-//   VGPRs and runs the serial part of a chunk step alone:
+//   the state wave (one per V tile) holds every key row of the tile's fp32
+//   state in VGPRs and runs the serial part of a chunk step alone:
 //       X = K S,  Y = V - e^G X,  vnew = Tb Y,
 //       S = e^G_last S + K^T (e^(G_last - G) vnew)
 //   (Tb = (I + A)^-1 diag(beta) from the prep kernel; K S, Tb Y and K^T U
@@ -12,13 +13,14 @@
 //   product's B operand where it stands (row orders below), so no LDS
 //   exchange sits inside the step, and every operand comes from LDS.
 //
-//   wave 1, the stage wave, loads chunk c+2's K rows and Tb fragments
-//   straight into LDS (buffer_load ... lds) while step c runs.
+//   the stage wave loads chunk c+2's K rows and Tb fragments straight into
+//   LDS (buffer_load ... lds) while step c runs.
 //
-//   wave 2, the output wave, writes chunk c+1's V tile (as fp32, in the
-//   state wave's layout) and gate factors into LDS and forms chunk c-1's
-//   output from the state and vnew fragments the state wave leaves in LDS:
-//       o = scale e^G (Q S) + P vnew.
+//   the output wave writes chunk c+1's V tiles (as fp32, in the state
+//   waves' layout) and gate factors into LDS and forms chunk c-1's output
+//   from the state and vnew fragments the state waves leave in LDS:
+//       o = scale e^G (Q S) + P vnew
+//   (with both the backward's saves and o, a save wave stores the former).
 //
 // One s_barrier per chunk step hands the buffers over (three stage buffers,
 // three output buffers).  The state wave issues no global load at all.
@@ -40,9 +42,12 @@ namespace gdn {
 // SAVE: store the state at every chunk start (ws.hs, bf16, transposed) and
 // the per-token delta vnew (ws.dl, bf16) for the backward.  OUT: write o and
 // ht.  Forward <K, false, true>, the backward's recomputation <K, true,
-// false>, a training forward <K, true, true>.
-template <int K, bool SAVE, bool OUT>
-__global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel(
+// false>, a training forward <K, true, true>.  NS: V tiles (slices) per
+// workgroup, one state wave each, sharing the stage wave's K / Tb buffers
+// and the output wave's Q / P (2 when there are enough chains to fill the
+// GPU twice over).
+template <int K, bool SAVE, bool OUT, int NS>
+__global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_chain_sw_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
@@ -58,16 +63,16 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
   using KL = KLayout<K>;
   __shared__ __attribute__((aligned(16))) unsigned char Kst[3][KL::BYTES];
   __shared__ __attribute__((aligned(16))) u16x8 Tst[3][6][2][64];
-  __shared__ __attribute__((aligned(16))) float Vst[3][4][4][68];
+  __shared__ __attribute__((aligned(16))) float Vst[3][NS][4][4][68];
   __shared__ __attribute__((aligned(16))) float Gst[3][2][64];
   __shared__ float Egl[3];
   // Output buffers (chunk c in buffer c % 3), left by the state wave for
   // the output wave: the state's hi B fragments at the chunk start and
   // vnew (bf16) as B fragments.
-  __shared__ __attribute__((aligned(16))) u16x8 Sx[3][KB][64];
-  __shared__ __attribute__((aligned(16))) u16x8 Vx[3][2][64];
+  __shared__ __attribute__((aligned(16))) u16x8 Sx[3][NS][KB][64];
+  __shared__ __attribute__((aligned(16))) u16x8 Vx[3][NS][2][64];
 
-  const int NVT = V / 16;
+  const int NVT = V / (16 * NS);   // workgroups per v-head
   // XCD-aware placement, as in the four-wave chain: a qk-head group's
   // workgroups stay on one XCD (shared K / Q / Tb / P in its L2), and the
   // groups are dealt round-robin so every XCD gets a share of each sequence.
@@ -80,7 +85,7 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
   } else if ((nb & 7) == 0) {
     bid = (bid & 7) * (nb >> 3) + (bid >> 3);
   }
-  const int vt = bid % NVT;
+  const int vt0 = (bid % NVT) * NS;   // first V tile of this workgroup
   const int h = (bid / NVT) % Hv;
   const int n = bid / NVT / Hv;
   const int hq = h / (Hv / Hqk);
@@ -94,8 +99,12 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
   const int c_begin = cu ? ws.off[n] : n * nct;
   const int nc = (cu ? ws.off[n + 1] : (n + 1) * nct) - c_begin;
 
-  if (w == 0) {
+  // the state wave of V tile `vs` (a compile-time index, so that its LDS
+  // addresses are immediates as with one tile per workgroup)
+  auto state_wave = [&](auto slc) {
+    constexpr int vs = decltype(slc)::value;
     // ------------------------------------------------------ state wave ----
+    const int vt = vt0 + vs;   // this wave's V tile
     // state tile t: lane (n16, grp), element r = S[rho(16t + 4grp + r)][16 vt + n16]
     const size_t tile = ((size_t)n * Hv + h) * (size_t)K * V + 16 * vt + r16;
     f32x4 S[ST];
@@ -146,7 +155,7 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
         const int r0 = 32 * (ti >> 1) + 8 * grp + 4 * (ti & 1);
         eg[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][0][r0]);
         dc[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][1][r0]);
-        vv[ti] = *reinterpret_cast<const f32x4*>(&Vst[b3][ti][grp][4 * r16]);
+        vv[ti] = *reinterpret_cast<const f32x4*>(&Vst[b3][vs][ti][grp][4 * r16]);
       }
       const float egl = Egl[b3];
 
@@ -161,7 +170,7 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
         split_bf4(S[2 * b], h0v, l0v);
         split_bf4(S[2 * b + 1], h1v, l1v);
         const u16x8 sh = cat8(h0v, h1v), sl = cat8(l0v, l1v);
-        Sx[b3][b][lane] = sh;   // for this chunk's Q S (output wave)
+        Sx[b3][vs][b][lane] = sh;   // for this chunk's Q S (output wave)
 #pragma unroll
         for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sh, X[ti]);
 #pragma unroll
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
         split_bf4(dc[2 * b] * vn[2 * b], hh0, ll0);
         split_bf4(dc[2 * b + 1] * vn[2 * b + 1], hh1, ll1);
         const u16x8 uh = cat8(hh0, hh1), ul = cat8(ll0, ll1);
-        Vx[b3][b][lane] = cat8(f2bf4(vn[2 * b]), f2bf4(vn[2 * b + 1]));
+        Vx[b3][vs][b][lane] = cat8(f2bf4(vn[2 * b]), f2bf4(vn[2 * b + 1]));
 #pragma unroll
         for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], uh, S[t]);
 #pragma unroll
@@ -249,7 +258,11 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
         for (int r = 0; r < 4; ++r) ht[tile + (size_t)rho_row(t, 4 * grp + r) * V] = S[t][r];
       }
     }
-  } else if (w == 1) {
+  };
+  if (w < NS) {
+    if (w == 0) state_wave(std::integral_constant<int, 0>{});
+    else state_wave(std::integral_constant<int, NS - 1>{});
+  } else if (w == NS) {
     // ------------------------------------------------------ stage wave ----
     // Issues chunk j+2's K rows and Tb fragments straight to LDS during step
     // j (buffer_load ... lds: 16 bytes per lane, 1 KiB per instruction, lane
@@ -326,16 +339,16 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
     // every step issues the same loads and stores, so each wait names an
     // exact count.
     constexpr int kQP = OUT ? 4 * KB + 6 : 0;   // Q / P loads per chunk
-    constexpr int kVG = 3;                      // V tile (2) + G (1)
-    // with both outputs, the saves go to a wave of their own (wave 3)
+    constexpr int kVG = 2 * NS + 1;             // V tiles (2 per slice) + G (1)
+    // with both outputs, the saves go to a wave of their own (the last)
     constexpr bool kSplit = SAVE && OUT;
-    constexpr int kSave = SAVE && !kSplit ? KB + 2 : 0;   // state and delta stores per chunk
-    constexpr int kStep = (OUT ? 4 : 0) + kSave + kQP + kVG;   // stores + loads per step
+    constexpr int kSave = SAVE && !kSplit ? NS * (KB + 2) : 0;   // state and delta stores per chunk
+    constexpr int kStep = (OUT ? 4 * NS : 0) + kSave + kQP + kVG;   // stores + loads per step
     const int rowq = Hqk * K * 2;
     struct Regs {
       u16x8 qf[4][KB];   // Q rows 16 ti + r16, B operand of (Q S)^T
       u16x8 pf[6];       // P fragments by tb_slot
-      u16x8 v0, v1;      // V tile row `lane`, 16 columns
+      u16x8 vr[NS][2];   // V tile row `lane`, 16 columns per slice
       float G;           // G of token `lane`
     };
     Regs rA, rB;
@@ -369,11 +382,15 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
       const int ci = c_begin + j;
       const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V + 16 * vt), 0,
-          (L - 1) * Hv * V * 2 + 32, kBufferFlags);
-      r.v0 = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * Hv * V * 2, 0, 0));
-      r.v1 = __builtin_bit_cast(u16x8,
-                                __builtin_amdgcn_raw_buffer_load_b128(rv, lane * Hv * V * 2 + 16, 0, 0));
+          const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V + 16 * vt0), 0,
+          (L - 1) * Hv * V * 2 + 32 * NS, kBufferFlags);
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+          r.vr[sl][x] = __builtin_bit_cast(
+              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * Hv * V * 2 + 32 * sl + 16 * x, 0, 0));
+      }
       const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<float*>(ws.gate + ((size_t)ci * Hv + h) * 64), 0, 256, kBufferFlags);
       r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
@@ -384,11 +401,14 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
       // token row t = lane sits at tile ti = 2 (t / 32) + (t / 4) % 2,
       // lane (n16, (t / 8) % 4), element t % 4 of the state wave's layout
       const int ti = 2 * (lane >> 5) + ((lane >> 2) & 1);
-      float* dst = &Vst[buf][ti][(lane >> 3) & 3][lane & 3];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        dst[4 * c] = bf2f(r.v0[c]);
-        dst[4 * (c + 8)] = bf2f(r.v1[c]);
+      for (int sl = 0; sl < NS; ++sl) {
+        float* dst = &Vst[buf][sl][ti][(lane >> 3) & 3][lane & 3];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          dst[4 * c] = bf2f(r.vr[sl][0][c]);
+          dst[4 * (c + 8)] = bf2f(r.vr[sl][1][c]);
+        }
       }
       const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
       const float eg = __expf(r.G);
@@ -402,10 +422,13 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
     auto save_chunk = [&](int j, bool live) {
       const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
       const int b3 = j % 3;
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+      const int vt = vt0 + sl;
       u16x8 sh[KB];
       if (live) {
 #pragma unroll
-        for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][b][lane];
+        for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][sl][b][lane];
       }
       const size_t ci = live ? (size_t)(c_begin + j) : 0;
       const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
@@ -422,7 +445,7 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
       u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
       if (live) {
         const uint16_t* src =
-            reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
+            reinterpret_cast<const uint16_t*>(&Vx[b3][sl][lane >> 5][16 * ((lane >> 3) & 3)]) +
             (lane & 7);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -433,6 +456,7 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
       const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr, drow, 0, 0);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), dr, drow + 16, 0, 0);
+      }
     };
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     // o^T tiles of chunk j: lane (r16, grp) holds token row 16 ti + r16,
@@ -442,38 +466,41 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
     auto output = [&](const Regs& r, int j, bool live) {
       const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
       const int b3 = j % 3;
-      u16x8 sh[KB], vx[2];
-      if (live) {
-#pragma unroll
-        for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][b][lane];
-        vx[0] = Vx[b3][0][lane];
-        vx[1] = Vx[b3][1][lane];
-      }
       if constexpr (SAVE && !kSplit) save_chunk(j, live);
       if constexpr (!OUT) return;
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
           o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-        u16x4 ov = {0, 0, 0, 0};
+      for (int sl = 0; sl < NS; ++sl) {
+        u16x8 sh[KB], vx[2];
         if (live) {
-          f32x4 qa = zero4(), qb = zero4();
 #pragma unroll
-          for (int b = 0; b < KB; b += 2) {
-            qa = mfma16(sh[b], r.qf[ti][b], qa);
-            qb = mfma16(sh[b + 1], r.qf[ti][b + 1], qb);
-          }
-          f32x4 pv = mfma16(vx[0], r.pf[tb_slot(ti, 0)], zero4());
-          if (ti >= 2) pv = mfma16(vx[1], r.pf[tb_slot(ti, 1)], pv);
-          const float egi = Gst[b3][0][16 * ti + r16];
-          ov = f2bf4((scale * egi) * (qa + qb) + pv);
+          for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][sl][b][lane];
+          vx[0] = Vx[b3][sl][0][lane];
+          vx[1] = Vx[b3][sl][1][lane];
         }
-        __builtin_amdgcn_raw_buffer_store_b64(
-            __builtin_bit_cast(u32x2, ov), orsrc,
-            (((16 * ti + r16) * Hv + h) * V + 16 * vt + 4 * grp) * 2, 0, 0);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) {
+          u16x4 ov = {0, 0, 0, 0};
+          if (live) {
+            f32x4 qa = zero4(), qb = zero4();
+#pragma unroll
+            for (int b = 0; b < KB; b += 2) {
+              qa = mfma16(sh[b], r.qf[ti][b], qa);
+              qb = mfma16(sh[b + 1], r.qf[ti][b + 1], qb);
+            }
+            f32x4 pv = mfma16(vx[0], r.pf[tb_slot(ti, 0)], zero4());
+            if (ti >= 2) pv = mfma16(vx[1], r.pf[tb_slot(ti, 1)], pv);
+            const float egi = Gst[b3][0][16 * ti + r16];
+            ov = f2bf4((scale * egi) * (qa + qb) + pv);
+          }
+          __builtin_amdgcn_raw_buffer_store_b64(
+              __builtin_bit_cast(u32x2, ov), orsrc,
+              (((16 * ti + r16) * Hv + h) * V + 16 * (vt0 + sl) + 4 * grp) * 2, 0, 0);
+        }
       }
     };
-    if (kSplit && w == 3) {
+    if (kSplit && w == NS + 2) {
       // the save wave: chunk j-1's state and deltas during step j
       __syncthreads();
       for (int j = 0; j < nc; ++j) {
@@ -515,12 +542,38 @@ __global__ __launch_bounds__(SAVE && OUT ? 256 : 192) void chunk_chain_sw_kernel
   }
 }
 
+// Compute units of the current device, looked up once per device.
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
 template <int K, bool SAVE, bool OUT>
 void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
                      float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
                      int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st) {
-  hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT>), dim3(N * Hv * (V / 16)), dim3(SAVE && OUT ? 256 : 192), 0,
-                     st, q, k, v, h0, ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  // two V tiles per workgroup once the chains fill the GPU twice over: the
+  // tiles share the stage and output waves' operand traffic, and every chain
+  // still has a state wave of its own (not with both outputs: a fifth wave
+  // would halve the register budget)
+  const long long chains = (long long)N * Hv * (V / 16);
+  constexpr int kExtra = SAVE && OUT ? 1 : 0;
+  if (!(SAVE && OUT) && V % 32 == 0 && chains >= 2LL * device_cus())
+    hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT, (SAVE && OUT) ? 1 : 2>),
+                       dim3((unsigned)(chains / 2)), dim3((4 + kExtra) * 64), 0, st, q, k, v, h0,
+                       ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+  else
+    hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT, 1>), dim3((unsigned)chains),
+                       dim3((3 + kExtra) * 64), 0, st, q, k, v, h0, ht, o, cu, N, T, total, Hqk,
+                       Hv, V, scale, ws);
 }
 
 template void launch_chain_sw<64, false, true>(const uint16_t*, const uint16_t*, const uint16_t*,
