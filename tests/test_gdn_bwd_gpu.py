@@ -262,3 +262,28 @@ def test_bwd_varlen_many_sequences(rocm_device):
 def test_bwd_long_context(rocm_device):
     """Config 4's slow decay over a 16384-token sequence (256 chunks), 1 qk-head -> 2 v-heads."""
     _case(rocm_device, 1, 16384, 1, 2, 128, 128, seed=51, decay=0.01, what="T16384 decay .01")
+
+
+def test_bwd_two_tiles_per_workgroup(rocm_device):
+    """Enough chains for two V tiles per workgroup in the recomputed forward
+    (chain with saves): parity against the oracle, and sequence 0's
+    gradients equal, bit for bit, those of the sequence run alone."""
+    from avelang_amd import chunk_gated_delta_rule_bwd
+    cus = torch.cuda.get_device_properties(rocm_device).multi_processor_count
+    Hqk, Hv, K, V = 2, 4, 128, 128
+    B = -(-2 * cus // (Hv * (V // 16)))
+    wl = W.make(B, 96, Hqk, Hv, K, V, seed=94, h0_scale=0.01)
+    do, dht = _grad_inputs(wl, 94)
+    a = wl.numpy()
+    ref = RB.chunked_bwd(a["q"], a["k"], a["v"], a["g"], a["beta"], do, dht,
+                         initial_state=a["initial_state"])
+    got = _gpu_bwd(wl, do, dht, rocm_device)
+    _check(got, ref, f"two tiles B{B}")
+    t = wl.torch(rocm_device)
+    one = chunk_gated_delta_rule_bwd(
+        t["q"][:1], t["k"][:1], t["v"][:1], t["g"][:1], t["beta"][:1],
+        torch.from_numpy(do[:1]).to(device=rocm_device, dtype=torch.bfloat16),
+        torch.from_numpy(dht[:1]).to(rocm_device), initial_state=t["initial_state"][:1])
+    torch.cuda.synchronize()
+    for name, x in zip(("dq", "dk", "dv", "dg", "dbeta", "dh0"), one):
+        assert torch.equal(got[name][:1], x), name

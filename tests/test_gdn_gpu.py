@@ -386,3 +386,27 @@ def test_golden_cfg0(rocm_device):
         o, s = fn(q, k, v, g, beta, output_final_state=True)
         torch.cuda.synchronize()
         _check(o, z["o"], s, z["state"], fn.__name__)
+
+
+# ------------------------------------------ two V tiles per workgroup --
+
+@pytest.mark.parametrize("K,V", [(128, 128), (64, 64)])
+def test_two_tiles_per_workgroup(rocm_device, K, V):
+    """With at least twice as many (sequence, v-head, V tile) chains as CUs
+    the chain runs two V tiles per workgroup.  Every sequence matches the
+    oracle, and sequence 0 equals, bit for bit, the same sequence run alone
+    (few chains: one tile per workgroup)."""
+    from avelang_amd import chunk_gated_delta_rule
+    Hqk, Hv = 4, 8
+    cus = torch.cuda.get_device_properties(rocm_device).multi_processor_count
+    B = -(-2 * cus // (Hv * (V // 16)))          # chains >= 2 x CUs
+    wl = W.make(B, 200, Hqk, Hv, K, V, seed=93, h0_scale=0.01)
+    o, s = _run_chunk(wl, rocm_device)
+    o_ref, s_ref = _oracle("chunk", wl)
+    _check(o, o_ref, s, s_ref, f"two tiles K{K} V{V} B{B}")
+    t = wl.torch(rocm_device)
+    o1, s1 = chunk_gated_delta_rule(t["q"][:1], t["k"][:1], t["v"][:1], t["g"][:1],
+                                    t["beta"][:1], initial_state=t["initial_state"][:1],
+                                    output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o[:1], o1) and torch.equal(s[:1], s1)
