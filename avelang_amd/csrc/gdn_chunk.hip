@@ -124,13 +124,15 @@ __device__ __forceinline__ void scale_frags(u16x8 (&f)[KB], float r) {
 
 // One workgroup per (chunk, v-head).  Wave w owns chunk rows 16w..16w+15.
 // BWD (the backward's recomputation) also writes T itself and the A-operand
-// fragments of Tb^T and P^T for the reverse chain.
-template <int K, bool BWD>
+// fragments of Tb^T and P^T for the reverse chain.  L2: use_qk_l2norm (a
+// compile-time flag: with one code path per form the compiler's waits for
+// the K / Q row loads never include the normalised rows' stores).
+template <int K, bool BWD, bool L2>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ g, const float* __restrict__ beta,
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, float scale,
-    int l2norm, ChunkWs ws, GateIn gate) {
+    ChunkWs ws, GateIn gate) {
   constexpr int KB = K / 32;
   // strictly lower 16 x 16 blocks of A only (block (bi, m), m < bi, at
   // bi (bi - 1) / 2 + m; row stride 20 keeps float4 rows aligned and the 16
@@ -203,11 +205,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       ka[b] = *reinterpret_cast<const u16x8*>(k + ro + 32 * b);
       qa[b] = *reinterpret_cast<const u16x8*>(q + ro + 32 * b);
     }
-    if (l2norm) {
+    if constexpr (L2) {
       // use_qk_l2norm: a row's K values sit in the 4 lanes r16 + 16 grp; the
       // normalised rows are rounded to bf16 (as a separate l2norm pass would
       // store them), and the first v-head of each qk-head group stores them
-      // for the chain
+      // for the chain (below)
       float sk = 0.f, sq = 0.f;
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
@@ -225,18 +227,21 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       const float rk = rsqrtf(sk + 1e-6f), rq = rsqrtf(sq + 1e-6f);
       scale_frags<KB>(ka, rk);
       scale_frags<KB>(qa, rq);
-      if (h % (Hv / Hqk) == 0 && 16 * w + r16 < L) {
-        const size_t wo = ((size_t)(t0 + 16 * w + r16) * Hqk + hq) * K + 8 * grp;
-#pragma unroll
-        for (int b = 0; b < KB; ++b) {
-          *reinterpret_cast<u16x8*>(ws.kn + wo + 32 * b) = ka[b];
-          *reinterpret_cast<u16x8*>(ws.qn + wo + 32 * b) = qa[b];
-        }
-      }
     }
 #pragma unroll
     for (int b = 0; b < KB; ++b)
       *reinterpret_cast<u16x8*>(&Ks[16 * w + r16][32 * b + 8 * grp]) = ka[b];
+    // the normalised rows for the chain, stored after the LDS writes above
+    // (stores count in the same in-order vector-memory counter as the loads,
+    // so a wait for ka ahead of them would also wait for these stores)
+    if (L2 && h % (Hv / Hqk) == 0 && 16 * w + r16 < L) {
+      const size_t wo = ((size_t)(t0 + 16 * w + r16) * Hqk + hq) * K + 8 * grp;
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        *reinterpret_cast<u16x8*>(ws.kn + wo + 32 * b) = ka[b];
+        *reinterpret_cast<u16x8*>(ws.qn + wo + 32 * b) = qa[b];
+      }
+    }
   }
   // gates: wave 0 scans g over the 64 rows (padding rows add 0) and shares
   // G and beta through LDS
@@ -513,9 +518,14 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
   if (cu)
     hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, st, cu, N, T, total,
                        (int)p.ncmax, ws.off, ws.status);
-  if (p.ncmax > 0)
-    hipLaunchKernelGGL((chunk_prep_kernel<K, BWD>), dim3((unsigned)p.ncmax, Hv), dim3(256), 0,
-                       st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, l2 ? 1 : 0, ws, gate);
+  if (p.ncmax > 0) {
+    if (l2)
+      hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, true>), dim3((unsigned)p.ncmax, Hv), dim3(256),
+                         0, st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws, gate);
+    else
+      hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, false>), dim3((unsigned)p.ncmax, Hv), dim3(256),
+                         0, st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws, gate);
+  }
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised
   launch_chain_sw<K, BWD, OUT>(l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
                                OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws, st);
