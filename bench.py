@@ -571,14 +571,18 @@ def pmc_summary(fetch_dir, write_dir, out_path):
     def total(pred):
         return sum(v["fetch_bytes"] + v["write_bytes"] for k, v in kern.items() if pred(k))
 
+    def named(k, *prefixes):
+        # template arguments after these (the l2norm form, V tiles per
+        # workgroup) do not change which launch of the path it is
+        return any(k.startswith("gdn::" + p) and k[len("gdn::" + p)] in ",>" for p in prefixes)
+
     res = {
-        "prefill": total(lambda k: ("chunk_prep_kernel<128, false>" in k
-                                    or "chunk_chain_sw_kernel<128, false, true>" in k)),
+        "prefill": total(lambda k: named(k, "chunk_prep_kernel<128, false",
+                                         "chunk_chain_sw_kernel<128, false, true")),
         "decode": total(lambda k: "recurrent_kernel<128, 128" in k),
-        "backward": total(lambda k: ("chunk_prep_kernel<128, true>" in k
-                                     or "chunk_chain_sw_kernel<128, true, false>" in k
-                                     or "chunk_rev_sw_kernel<128>" in k
-                                     or "chunk_grad_kernel<128, 128>" in k)),
+        "backward": total(lambda k: named(k, "chunk_prep_kernel<128, true",
+                                          "chunk_chain_sw_kernel<128, true, false",
+                                          "chunk_rev_sw_kernel<128", "chunk_grad_kernel<128, 128")),
         "per_kernel": kern,
         "fetch_size_factor": round(ff, 4),
         "write_size_factor": round(wf, 4),
