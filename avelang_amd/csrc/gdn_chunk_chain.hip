@@ -344,6 +344,11 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     constexpr bool kSplit = SAVE && OUT;
     constexpr int kSave = SAVE && !kSplit ? NS * (KB + 2) : 0;   // state and delta stores per chunk
     constexpr int kStep = (OUT ? 4 * NS : 0) + kSave + kQP + kVG;   // stores + loads per step
+    // Without o the V / G loads go before the saves, and the step's wait
+    // lets the previous step's saves stay in flight as well (the counter
+    // retires loads and stores in issue order): the stores then have two
+    // steps to drain instead of one, measured 2.5 % off the backward
+    constexpr int kWait = OUT ? kStep : kStep + kSave;
     const int rowq = Hqk * K * 2;
     struct Regs {
       u16x8 qf[4][KB];   // Q rows 16 ti + r16, B operand of (Q S)^T
@@ -416,27 +421,35 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       Gst[buf][1][lane] = __expf(GL - r.G);
       if (lane == L - 1) Egl[buf] = eg;
     };
-    // SAVE: the chunk's start state (hs[chunk][v-head] = S^T, [V][K]: the
-    // state fragments as they stand, 16 bytes per k-block) and its deltas
-    // (dl, token-major); live = false stores to empty resources (dropped)
+    // SAVE: the chunk's start state (hs[chunk][v-head] = S^T, [V][K], the
+    // hi fragments) and its deltas (dl, token-major); live = false stores
+    // to empty resources (dropped)
     auto save_chunk = [&](int j, bool live) {
       const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
       const int b3 = j % 3;
 #pragma unroll
       for (int sl = 0; sl < NS; ++sl) {
       const int vt = vt0 + sl;
+      // store i, lane l: row 16 vt + rpi i + l / cpr, columns 8 (l % cpr)
+      // .. + 7, i.e. rpi whole rows per store (fragment lane r16 + 16 grp
+      // of k-block b holds row r16, columns 32 b + 8 grp .. + 7); whole
+      // rows measured 2 % faster than four 64-byte pieces of 16 rows
+      constexpr int cpr = K / 8, rpi = 64 / cpr;
+      const int c8 = lane % cpr;
       u16x8 sh[KB];
       if (live) {
 #pragma unroll
-        for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][sl][b][lane];
+        for (int i = 0; i < KB; ++i)
+          sh[i] = Sx[b3][sl][c8 >> 2][(rpi * i + lane / cpr) + 16 * (c8 & 3)];
       }
       const size_t ci = live ? (size_t)(c_begin + j) : 0;
       const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
           ws.hs + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
 #pragma unroll
-      for (int b = 0; b < KB; ++b)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sh[b]), hr,
-                                               ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
+      for (int i = 0; i < KB; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sh[i]), hr,
+                                               ((16 * vt + rpi * i + lane / cpr) * K + 8 * c8) * 2,
+                                               0, 0);
       // deltas: lane t gathers token row t (its 16 columns) from the vnew
       // fragments in LDS -- element (t % 8) of fragment lane 16 ((t / 8) % 4)
       // + n of k-block t / 32 -- and writes it with two 16-byte stores
@@ -518,15 +531,21 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       output(rA, 0, false);             // the stores a step issues, dropped
       load_qp(rA, 0);
       load_vg(rA, min(2, nc - 1));
+      if constexpr (!OUT) output(rA, 0, false);   // the previous step's saves
     }
     __syncthreads();
     // step j works on register set (j + 1) % 2
     auto step = [&](int j, Regs& r) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kStep));   // chunk j-1's Q / P, chunk j+1's V / G
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWait));   // chunk j-1's Q / P, chunk j+1's V / G
       if (j + 1 < nc) write_vg(r, j + 1);
-      output(r, j - 1, j >= 1);
-      load_qp(r, min(j + 1, nc - 1));
-      load_vg(r, min(j + 3, nc - 1));
+      if constexpr (OUT) {
+        output(r, j - 1, j >= 1);
+        load_qp(r, min(j + 1, nc - 1));
+        load_vg(r, min(j + 3, nc - 1));
+      } else {
+        load_vg(r, min(j + 3, nc - 1));
+        output(r, j - 1, j >= 1);
+      }
       __syncthreads();
     };
     int j = 0;
