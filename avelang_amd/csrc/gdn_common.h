@@ -155,14 +155,27 @@ struct GateIn {
 // past the end, 0).  The same value as ldp; a kernel that keeps loads in
 // flight across this one needs it, since a branch here would make the wait
 // at the join cover every outstanding load.
-__device__ __forceinline__ float ldp_flat(const void* p, long long i, int dt, long long n) {
+// The two raw words (issued now) and the value they give (formed later):
+// a kernel can load early and select when the value is needed.
+struct FlatRaw {
+  uint16_t h;
+  uint32_t w;
+};
+__device__ __forceinline__ FlatRaw ldp_flat_raw(const void* p, long long i, int dt, long long n) {
   const int es = dt == GDN_DTYPE_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<void*>(p), 0, static_cast<int>(n * es), kBufferFlags);
-  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(i * 2), 0, 0);
-  const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(i * 4), 0, 0);
-  const float hf = static_cast<float>(__builtin_bit_cast(_Float16, h));
-  return dt == GDN_DTYPE_F32 ? __uint_as_float(w) : (dt == GDN_DTYPE_BF16 ? bf2f(h) : hf);
+      const_cast<void*>(p), 0, p ? static_cast<int>(n * es) : 0, kBufferFlags);
+  FlatRaw x;
+  x.h = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(i * 2), 0, 0);
+  x.w = __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(i * 4), 0, 0);
+  return x;
+}
+__device__ __forceinline__ float flat_value(FlatRaw x, int dt) {
+  const float hf = static_cast<float>(__builtin_bit_cast(_Float16, x.h));
+  return dt == GDN_DTYPE_F32 ? __uint_as_float(x.w) : (dt == GDN_DTYPE_BF16 ? bf2f(x.h) : hf);
+}
+__device__ __forceinline__ float ldp_flat(const void* p, long long i, int dt, long long n) {
+  return flat_value(ldp_flat_raw(p, i, dt, n), dt);
 }
 
 // The per-head part (-exp(A_log[h]), dt_bias[h]) and the per-element part,
@@ -173,11 +186,10 @@ __device__ __forceinline__ void gate_head(const GateIn& p, int h, float& neg_a, 
   neg_a = -expf(FLAT ? ldp_flat(p.A_log, h, p.pdt, p.H) : ldp(p.A_log, h, p.pdt));
   dtb = FLAT ? ldp_flat(p.dt_bias, h, p.pdt, p.H) : ldp(p.dt_bias, h, p.pdt);
 }
-template <bool FLAT = false>
-__device__ __forceinline__ void gate_elem(const GateIn& p, long long i, float neg_a, float dtb,
-                                          float& g, float& beta) {
-  const float av = FLAT ? ldp_flat(p.a, i, p.adt, p.n) : ldp(p.a, i, p.adt);
-  const float bv = FLAT ? ldp_flat(p.b, i, p.bdt, p.n) : (p.b ? ldp(p.b, i, p.bdt) : 0.f);
+// g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) from the loaded
+// values (neg_a = -exp(A_log))
+__device__ __forceinline__ void gate_math(const GateIn& p, float neg_a, float dtb, float av,
+                                          float bv, float& g, float& beta) {
   const float x = av + dtb;
   const float bx = p.spb * x;
   // both sides formed, then selected (no branch; the clamp changes nothing
@@ -186,6 +198,31 @@ __device__ __forceinline__ void gate_elem(const GateIn& p, long long i, float ne
   const float sp = bx > p.spt ? x : lp;
   g = neg_a * sp;
   beta = 1.f / (1.f + expf(-bv));
+}
+template <bool FLAT = false>
+__device__ __forceinline__ void gate_elem(const GateIn& p, long long i, float neg_a, float dtb,
+                                          float& g, float& beta) {
+  const float av = FLAT ? ldp_flat(p.a, i, p.adt, p.n) : ldp(p.a, i, p.adt);
+  const float bv = FLAT ? ldp_flat(p.b, i, p.bdt, p.n) : (p.b ? ldp(p.b, i, p.bdt) : 0.f);
+  gate_math(p, neg_a, dtb, av, bv, g, beta);
+}
+// gate_at's loads issued ahead of its math (gate_eval, the same values)
+struct GateRaw {
+  FlatRaw A, d, a, b;
+};
+__device__ __forceinline__ GateRaw gate_load(const GateIn& p, long long i, int h) {
+  GateRaw r;
+  r.A = ldp_flat_raw(p.A_log, h, p.pdt, p.H);
+  r.d = ldp_flat_raw(p.dt_bias, h, p.pdt, p.H);
+  r.a = ldp_flat_raw(p.a, i, p.adt, p.n);
+  r.b = ldp_flat_raw(p.b, i, p.bdt, p.n);
+  return r;
+}
+__device__ __forceinline__ void gate_eval(const GateIn& p, const GateRaw& r, float& g,
+                                          float& beta) {
+  const float neg_a = -expf(flat_value(r.A, p.pdt));
+  gate_math(p, neg_a, flat_value(r.d, p.pdt), flat_value(r.a, p.adt), flat_value(r.b, p.bdt), g,
+            beta);
 }
 __device__ __forceinline__ void gate_at(const GateIn& p, long long i, int h, float& g,
                                         float& beta) {

@@ -64,6 +64,7 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
 
   __shared__ float kq_s[2][K];
   __shared__ float red[NW][COLG][NRED + 1];
+  __shared__ float gsh[2];   // GATE: g, beta of a tile's first token
 
   const int tid = threadIdx.x;
   const int cg = tid % COLG;
@@ -92,8 +93,15 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     }
     return slot;
   };
-  auto load_state = [&](f32x4 (&S)[RPT], int tile) {
+  // GATE: the tile's first-token gate inputs are loaded with its state (and
+  // ahead of it), one tile before they are used
+  auto load_state = [&](f32x4 (&S)[RPT], GateRaw& gr, int tile) {
     const int tl = min(tile, ntiles - 1);
+    if constexpr (GATE) {
+      const int n = tl / Hv;
+      const int s = cu ? min(max(cu[n], 0), total_tokens) : n * T;
+      gr = gate_load(gate, (long long)s * Hv + tl % Hv, tl % Hv);
+    }
     const int slot = slot_of(tl);
     const bool live = h0 && tile < ntiles && slot >= 0;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -105,7 +113,7 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
           rs, ((rg + ROWG * i) * COLG + cg) * 16, 0, kNonTemporal));
   };
 
-  auto run_tile = [&](f32x4 (&S)[RPT], int tile) {
+  auto run_tile = [&](f32x4 (&S)[RPT], const GateRaw& gr, int tile) {
     const int slot = slot_of(tile);
     if (slot < 0) return;
     const int h = tile % Hv;
@@ -120,6 +128,18 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
       e = s + T;
     }
     for (int t = s; t < e; ++t) {
+      if (GATE && t == s && wave == NW - 1) {
+        // the first token's gate, from inputs loaded a tile ahead: formed
+        // by the one wave that stages no k / q row, before the loads whose
+        // wait would also cover the next tile's state prefetch, so the math
+        // overlaps that prefetch; shared through LDS at the barrier below
+        float g0, b0;
+        gate_eval(gate, gr, g0, b0);
+        if (lane == 0) {
+          gsh[0] = g0;
+          gsh[1] = b0;
+        }
+      }
       const size_t qk_row = ((size_t)t * Hqk + hq) * K;
       // speculative decoding: slot receiving the state after this token
       int tslot = -1;
@@ -133,19 +153,23 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
       }
       const size_t vh = (size_t)t * Hv + h;
       const u16x4 vb = *reinterpret_cast<const u16x4*>(v + vh * V + 4 * cg);
-      float gt, bt;
+      float gt = 0.f, bt = 0.f;
       if constexpr (GATE) {
-        // formed where the other form reads g and beta (a load whose result
-        // is needed at the tile start would wait for the next tile's state
-        // prefetch, issued just before)
-        float neg_a, dtb;
-        gate_head<true>(gate, h, neg_a, dtb);
-        gate_elem<true>(gate, (long long)vh, neg_a, dtb, gt, bt);
+        // later tokens (multi-token steps): formed here
+        if (t > s) {
+          float neg_a, dtb;
+          gate_head<true>(gate, h, neg_a, dtb);
+          gate_elem<true>(gate, (long long)vh, neg_a, dtb, gt, bt);
+        }
       } else {
         gt = g[vh];
         bt = beta[vh];
       }
       __syncthreads();
+      if (GATE && t == s) {
+        gt = gsh[0];
+        bt = gsh[1];
+      }
 
       float r[NRED];
       float kreg[RPT];  // k rows kept in VGPRs: kq_s is restaged by the next token
@@ -223,14 +247,15 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
   int t = blockIdx.x;
   if (t >= ntiles) return;
   f32x4 SA[RPT], SB[RPT];
-  load_state(SA, t);
+  GateRaw gA{}, gB{};
+  load_state(SA, gA, t);
   for (;;) {
-    load_state(SB, t + G);
-    run_tile(SA, t);
+    load_state(SB, gB, t + G);
+    run_tile(SA, gA, t);
     t += G;
     if (t >= ntiles) break;
-    load_state(SA, t + G);
-    run_tile(SB, t);
+    load_state(SA, gA, t + G);
+    run_tile(SB, gB, t);
     t += G;
     if (t >= ntiles) break;
   }
