@@ -205,12 +205,19 @@ def cpu_backward(wl, runs=3):
                 host=host)
 
 
+# Workload seeds of the extra prefill lines.  Config 3's lengths are drawn
+# uniform in [128, 4096] from the seed; seed 5 gives 134,847 tokens, the
+# draw of seeds 0-11 closest to the ~134k the configuration names (seed 1,
+# used before, gave 116,494).
+EXTRA_SEEDS = {"cfg3_varlen_64seq": 5, "cfg4_long_context": 1}
+
+
 def bench_prefill_config(dev, name, reps=3):
     """One eager call per repetition of another prefill config (median ms)."""
     from avelang_amd import chunk_gated_delta_rule
     from avelang_amd import workloads as W
 
-    wl = W.config(name, seed=1)
+    wl = W.config(name, seed=EXTRA_SEEDS.get(name, 1))
     t = wl.torch(dev)
 
     def call():
