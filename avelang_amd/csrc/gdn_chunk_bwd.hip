@@ -65,6 +65,18 @@ struct BwdWs {
 // s + 3 is already requested into registers.
 constexpr int kGradThreads = 512;
 
+// Sum over the 16 lanes of a row (lanes 16 g .. 16 g + 15), every lane of
+// the row receiving it: within quads (lane ^ 1, lane ^ 2), then the
+// half-row mirror (lane i <- 7 - i) and the row mirror (lane i <- 15 - i),
+// as DPP moves: no LDS traffic, unlike a shuffle.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true));
+  return x;
+}
+
 template <int K, int V>
 __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -103,11 +115,14 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   uint16_t (*dds)[LV] = reinterpret_cast<uint16_t (*)[LV]>(regA);
   uint16_t (*R2s)[LK] = reinterpret_cast<uint16_t (*)[LK]>(regB);
   uint16_t (*Ms)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regB);
+  // dv rows of a v-head (bf16), staged in the slice stage once the slices are done
+  uint16_t (*Dvs)[LV] = reinterpret_cast<uint16_t (*)[LV]>(StgRaw);
+  static_assert(64 * LV * 2 <= kStgBytes, "dv rows must fit in the slice stage");
   uint16_t (*MPs)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regA);
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
-  __shared__ __attribute__((aligned(16))) float Cs[64];     // column sums of X
-  __shared__ __attribute__((aligned(16))) float Cv[64];     // column sums of T * (dd V^T)
+  // column partial sums over 8-row parts: of X (0) and of T * (dd V^T) (1)
+  __shared__ __attribute__((aligned(16))) float ColP[2][8][64];
   __shared__ __attribute__((aligned(16))) float RowP[2][5][64];   // row partials per half
   __shared__ float Red[8];
 
@@ -426,8 +441,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       u16x8 ta[2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) ta[b] = lds_colfrag(&Tb16[0][0], LC, 32 * b, 16 * rt, lane);
-      const __amdgpu_buffer_rsrc_t rdv = __builtin_amdgcn_make_buffer_rsrc(
-          dv + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+      // dv into the (free) slice stage as bf16 rows, stored after the
+      // barrier below with 16 bytes per thread
 #pragma unroll
       for (int m = 0; m < VH; ++m) {
         const int ct = 2 * m + hf;
@@ -436,9 +451,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         for (int b = 0; b < 2; ++b)
           tu = mfma16(ta[b], lds_colfrag(&dds[0][0], LV, 32 * b, 16 * ct, lane), tu);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          __builtin_amdgcn_raw_buffer_store_b16(f2bf(bt[r] * tu[r]), rdv,
-                                                ((row0 + r) * Hv * V + 16 * ct + r16) * 2, 0, 0);
+        for (int r = 0; r < 4; ++r) Dvs[row0 + r][16 * ct + r16] = f2bf(bt[r] * tu[r]);
       }
 #pragma unroll
       for (int m = 0; m < KH; ++m) {
@@ -455,7 +468,18 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         }
       }
     }
-    __syncthreads();   // X32 = dT complete; dd / R2 no longer needed
+    __syncthreads();   // X32 = dT complete; dd / R2 no longer needed; dv staged
+    {
+      const __amdgpu_buffer_rsrc_t rdv = __builtin_amdgcn_make_buffer_rsrc(
+          dv + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+#pragma unroll
+      for (int i = 0; i < 64 * V / 8 / NTH; ++i) {
+        const int p = tid + NTH * i, r = p / (V / 8), c8 = 8 * (p % (V / 8));
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, *reinterpret_cast<const u16x8*>(&Dvs[r][c8])), rdv,
+            (r * Hv * V + c8) * 2, 0, 0);
+      }
+    }
 
     // ---- dA = strict_lower(-T^T (dT T^T)) on fp32 MFMA (T lower triangular)
     f32x4 m1[2];
@@ -506,7 +530,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         }
       }
     }
-    // ---- C x C elementwise: M, MP, dbeta / dG terms, X; T * (dd V^T) for Cv
+    // ---- C x C elementwise: M, MP, dbeta / dG terms, X; T * (dd V^T) for the column sums
     f32x4 dba = zero4(), xr = zero4();
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
@@ -528,14 +552,17 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
     }
     __syncthreads();
-    if (tid < 64) {
+    {
+      // every thread: column tid % 64 over the 8 rows of part tid / 64
+      const int col = tid & 63, part = tid >> 6;
       float c = 0.f, cv = 0.f;
-      for (int i = 0; i < 64; ++i) {
-        c += X32[i][tid];
-        cv += T32[i][tid];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        c += X32[8 * part + i][col];
+        cv += T32[8 * part + i][col];
       }
-      Cs[tid] = c;
-      Cv[tid] = cv;
+      ColP[0][part][col] = c;
+      ColP[1][part][col] = cv;
     }
 
     if constexpr (decltype(prefetch_next)::value) issue_stage(gi + 1);
@@ -571,15 +598,12 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     // ---- row partials: reduce over the 16 lanes of a group, then combine
     // the two column halves through LDS
 #pragma unroll
-    for (int sh = 1; sh < 16; sh *= 2) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        qr1[r] += __shfl_xor(qr1[r], sh);
-        rho[r] += __shfl_xor(rho[r], sh);
-        ktw[r] += __shfl_xor(ktw[r], sh);
-        dba[r] += __shfl_xor(dba[r], sh);
-        xr[r] += __shfl_xor(xr[r], sh);
-      }
+    for (int r = 0; r < 4; ++r) {
+      qr1[r] = row16_sum(qr1[r]);
+      rho[r] = row16_sum(rho[r]);
+      ktw[r] = row16_sum(ktw[r]);
+      dba[r] = row16_sum(dba[r]);
+      xr[r] = row16_sum(xr[r]);
     }
     if (r16 == 0) {
       *reinterpret_cast<f32x4*>(&RowP[hf][0][row0]) = qr1;
@@ -591,7 +615,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
 #pragma unroll
     for (int sh = 1; sh < 64; sh *= 2) sde += __shfl_xor(sde, sh);
     if (lane == 0) Red[w8] = sde;
-    __syncthreads();   // Cs, Cv, RowP, Red complete
+    __syncthreads();   // ColP, RowP, Red complete
     if (w8 == 0) {
       // per row (lane = row): total dG and dbeta, then dg = reverse cumsum
       const int i = lane;
@@ -606,10 +630,16 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       float rho_all = rrho;
 #pragma unroll
       for (int sh = 1; sh < 64; sh *= 2) rho_all += __shfl_xor(rho_all, sh);
+      float csum = 0.f, cvsum = 0.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        csum += ColP[0][x][i];
+        cvsum += ColP[1][x][i];
+      }
       const float egi = __expf(Gs[i]), bi = Bs[i];
-      float dG = egi * rq1 - rrho + bi * egi * rktw + rxr - Cs[i];
+      float dG = egi * rq1 - rrho + bi * egi * rktw + rxr - csum;
       if (i == L - 1) dG += __expf(GL) * sd + rho_all;
-      if (i < L) dbeta[(size_t)(t0 + i) * Hv + h] = Cv[i] + egi * rktw + rdba;
+      if (i < L) dbeta[(size_t)(t0 + i) * Hv + h] = cvsum + egi * rktw + rdba;
       float x = i < L ? dG : 0.f;
       // reverse inclusive scan over the 64 rows
       x = __shfl(x, 63 - lane);
@@ -653,14 +683,11 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
     }
 #pragma unroll
-    for (int sh = 1; sh < 16; sh *= 2) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sq[r] += __shfl_xor(sq[r], sh);
-        sk[r] += __shfl_xor(sk[r], sh);
-        pq[r] += __shfl_xor(pq[r], sh);
-        pk[r] += __shfl_xor(pk[r], sh);
-      }
+    for (int r = 0; r < 4; ++r) {
+      sq[r] = row16_sum(sq[r]);
+      sk[r] = row16_sum(sk[r]);
+      pq[r] = row16_sum(pq[r]);
+      pk[r] = row16_sum(pk[r]);
     }
     // combine the two column halves (RowP is free after the v-head loop)
     if (r16 == 0) {
@@ -684,15 +711,29 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
     }
   }
+  // dq, dk rows through LDS (X32 / T32, free after the last v-head), then
+  // 16 bytes per thread
+  uint16_t (*Dqs)[LK] = reinterpret_cast<uint16_t (*)[LK]>(&X32[0][0]);
+  uint16_t (*Dks)[LK] = reinterpret_cast<uint16_t (*)[LK]>(&T32[0][0]);
+  static_assert(64 * LK * 2 <= 64 * LT * 4, "dq / dk rows must fit in X32 / T32");
 #pragma unroll
   for (int m = 0; m < KH; ++m) {
     const int ct = 2 * m + hf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dQa[m][r]), rdq, off, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dKa[m][r]), rdk, off, 0, 0);
+      Dqs[row0 + r][16 * ct + r16] = f2bf(dQa[m][r]);
+      Dks[row0 + r][16 * ct + r16] = f2bf(dKa[m][r]);
     }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 64 * K / 8 / NTH; ++i) {
+    const int p = tid + NTH * i, r = p / (K / 8), c8 = 8 * (p % (K / 8));
+    const int off = (r * Hqk * K + c8) * 2;
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(u32x4, *reinterpret_cast<const u16x8*>(&Dqs[r][c8])), rdq, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(u32x4, *reinterpret_cast<const u16x8*>(&Dks[r][c8])), rdk, off, 0, 0);
   }
 }
 
