@@ -114,3 +114,36 @@ def test_decode_fused_gating_slot_pool(rocm_device):
     live = torch.ones(N, dtype=torch.bool)
     live[3] = False
     assert torch.equal(o1[live], o2[live]) and torch.equal(p1, p2)
+
+
+@pytest.mark.parametrize("l2", [False, True])
+def test_decode_fused_gating_varlen(rocm_device, l2):
+    """Packed sequences of 3, 0, 1, 6, 0 and 7 tokens: a sequence's first-token
+    gate is loaded a tile ahead and formed by one wave, later tokens' gates in
+    place; empty sequences keep their state."""
+    from avelang_amd import (fused_gdn_gating, fused_recurrent_gated_delta_rule,
+                             fused_recurrent_gated_delta_rule_gated)
+    cu = np.array([0, 3, 3, 4, 10, 10, 17], dtype=np.int32)
+    wl = W.make(1, 17, 4, 8, 128, 128, seed=87, h0_scale=0.05, cu_seqlens=cu, l2norm=not l2)
+    t = wl.torch(rocm_device)
+    a, b, A_log, dt_bias = _gates(rocm_device, 1, 17, 8, 88)
+    g, beta = fused_gdn_gating(A_log, a, b, dt_bias)
+    s1 = t["initial_state"].clone()
+    s2 = t["initial_state"].clone()
+    kw = dict(output_final_state=True, cu_seqlens=t["cu_seqlens"], use_qk_l2norm_in_kernel=l2)
+    o1, _ = fused_recurrent_gated_delta_rule(t["q"], t["k"], t["v"], g, beta, initial_state=s1,
+                                             **kw)
+    o2, _ = fused_recurrent_gated_delta_rule_gated(t["q"], t["k"], t["v"], a, b, A_log, dt_bias,
+                                                   initial_state=s2, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    # the decode kernel normalises q, k in fp32 inside its dot products (no
+    # bf16 rounding of the normalised rows), as the oracle's own l2norm does
+    gg, bb = LR.gating(A_log.float().cpu().numpy(), a.float().cpu().numpy(),
+                       b.float().cpu().numpy(), dt_bias.float().cpu().numpy())
+    n = wl.numpy()
+    n["g"], n["beta"] = gg.astype(np.float32), bb.astype(np.float32)
+    o_ref, s_ref = oracle.run("recurrent", **n, use_qk_l2norm=l2)
+    err = np.abs(o2.float().cpu().numpy() - o_ref)
+    assert (err <= O_TOL + O_TOL * np.abs(o_ref)).all(), f"o max err {err.max():.3e}"
+    assert _fro(s2.cpu().numpy(), s_ref) <= S_FRO
