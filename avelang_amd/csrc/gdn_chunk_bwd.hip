@@ -115,9 +115,6 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   uint16_t (*dds)[LV] = reinterpret_cast<uint16_t (*)[LV]>(regA);
   uint16_t (*R2s)[LK] = reinterpret_cast<uint16_t (*)[LK]>(regB);
   uint16_t (*Ms)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regB);
-  // dv rows of a v-head (bf16), staged in the slice stage once the slices are done
-  uint16_t (*Dvs)[LV] = reinterpret_cast<uint16_t (*)[LV]>(StgRaw);
-  static_assert(64 * LV * 2 <= kStgBytes, "dv rows must fit in the slice stage");
   uint16_t (*MPs)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regA);
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
@@ -441,8 +438,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       u16x8 ta[2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) ta[b] = lds_colfrag(&Tb16[0][0], LC, 32 * b, 16 * rt, lane);
-      // dv into the (free) slice stage as bf16 rows, stored after the
-      // barrier below with 16 bytes per thread
+      const __amdgpu_buffer_rsrc_t rdv = __builtin_amdgcn_make_buffer_rsrc(
+          dv + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
 #pragma unroll
       for (int m = 0; m < VH; ++m) {
         const int ct = 2 * m + hf;
@@ -451,7 +448,9 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         for (int b = 0; b < 2; ++b)
           tu = mfma16(ta[b], lds_colfrag(&dds[0][0], LV, 32 * b, 16 * ct, lane), tu);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Dvs[row0 + r][16 * ct + r16] = f2bf(bt[r] * tu[r]);
+        for (int r = 0; r < 4; ++r)
+          __builtin_amdgcn_raw_buffer_store_b16(f2bf(bt[r] * tu[r]), rdv,
+                                                ((row0 + r) * Hv * V + 16 * ct + r16) * 2, 0, 0);
       }
 #pragma unroll
       for (int m = 0; m < KH; ++m) {
@@ -468,18 +467,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         }
       }
     }
-    __syncthreads();   // X32 = dT complete; dd / R2 no longer needed; dv staged
-    {
-      const __amdgpu_buffer_rsrc_t rdv = __builtin_amdgcn_make_buffer_rsrc(
-          dv + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
-#pragma unroll
-      for (int i = 0; i < 64 * V / 8 / NTH; ++i) {
-        const int p = tid + NTH * i, r = p / (V / 8), c8 = 8 * (p % (V / 8));
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(u32x4, *reinterpret_cast<const u16x8*>(&Dvs[r][c8])), rdv,
-            (r * Hv * V + c8) * 2, 0, 0);
-      }
-    }
+    __syncthreads();   // X32 = dT complete; dd / R2 no longer needed
 
     // ---- dA = strict_lower(-T^T (dT T^T)) on fp32 MFMA (T lower triangular)
     f32x4 m1[2];
@@ -711,29 +699,15 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
     }
   }
-  // dq, dk rows through LDS (X32 / T32, free after the last v-head), then
-  // 16 bytes per thread
-  uint16_t (*Dqs)[LK] = reinterpret_cast<uint16_t (*)[LK]>(&X32[0][0]);
-  uint16_t (*Dks)[LK] = reinterpret_cast<uint16_t (*)[LK]>(&T32[0][0]);
-  static_assert(64 * LK * 2 <= 64 * LT * 4, "dq / dk rows must fit in X32 / T32");
 #pragma unroll
   for (int m = 0; m < KH; ++m) {
     const int ct = 2 * m + hf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      Dqs[row0 + r][16 * ct + r16] = f2bf(dQa[m][r]);
-      Dks[row0 + r][16 * ct + r16] = f2bf(dKa[m][r]);
+      const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dQa[m][r]), rdq, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dKa[m][r]), rdk, off, 0, 0);
     }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 64 * K / 8 / NTH; ++i) {
-    const int p = tid + NTH * i, r = p / (K / 8), c8 = 8 * (p % (K / 8));
-    const int off = (r * Hqk * K + c8) * 2;
-    __builtin_amdgcn_raw_buffer_store_b128(
-        __builtin_bit_cast(u32x4, *reinterpret_cast<const u16x8*>(&Dqs[r][c8])), rdq, off, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b128(
-        __builtin_bit_cast(u32x4, *reinterpret_cast<const u16x8*>(&Dks[r][c8])), rdk, off, 0, 0);
   }
 }
 
