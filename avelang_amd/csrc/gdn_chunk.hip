@@ -31,6 +31,7 @@
 // hi+lo bf16 splits of their fp32 operand(s); Q S and P vnew (output only)
 // use single bf16.
 #include <mutex>
+#include <type_traits>
 
 #include "gdn_chunk.h"
 
@@ -111,6 +112,27 @@ void launch_zero_on_violation(const int32_t* status, const ZeroList& z, hipStrea
 
 // ---------------------------------------------------------- prep (K1) ----
 constexpr int kLdA = 68;   // fp32 row stride of A / Tm in LDS (rows 16-byte aligned)
+
+// Inclusive prefix sum over the 64 lanes as DPP moves: within each 16-lane
+// row by shifts to the right (lanes before the row's start read 0), then
+// the last lane of row 0 and of row 2 is added to rows 1 and 3 (row_bcast15)
+// and the last lane of row 1 to rows 2 and 3 (row_bcast31).
+__device__ __forceinline__ float prefix_sum64(float x) {
+  auto shr = [](float v, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                decltype(ctrl)::value, 0xF, 0xF,
+                                                                true));
+  };
+  x += shr(x, std::integral_constant<int, 0x111>{});
+  x += shr(x, std::integral_constant<int, 0x112>{});
+  x += shr(x, std::integral_constant<int, 0x114>{});
+  x += shr(x, std::integral_constant<int, 0x118>{});
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142,
+                                                             0xA, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143,
+                                                             0xC, 0xF, false));
+  return x;
+}
 
 // Rows of MFMA fragments scaled by r and rounded back to bf16.
 template <int KB>
@@ -248,11 +270,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   if (w == 0) {
     gv = lane < L ? gv : 0.f;
     bv = lane < L ? bv : 0.f;
-#pragma unroll
-    for (int d = 1; d < 64; d *= 2) {
-      const float o = __shfl_up(gv, d);
-      if (lane >= d) gv += o;
-    }
+    gv = prefix_sum64(gv);
     ws.gate[((size_t)ci * Hv + h) * 64 + lane] = gv;
     Gs[lane] = gv;
     Bs[lane] = bv;

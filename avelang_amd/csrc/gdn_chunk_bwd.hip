@@ -77,6 +77,35 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Sum over all 64 lanes (row sums, then the four row totals read from lanes
+// 0, 16, 32, 48), the same value in every lane.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  const int xi = __builtin_bit_cast(int, x);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48)));
+}
+
+// Suffix sums over the 64 lanes: lane i receives x_i + ... + x_63.  Within
+// each 16-lane row by DPP row shifts to the left (lanes past the row's end
+// read 0), then each row adds the totals of the rows above it (their first
+// lanes, read with readlane).
+__device__ __forceinline__ float suffix_sum(float x, int lane) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x101, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x102, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x104, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x108, 0xF, 0xF, true));
+  const int xi = __builtin_bit_cast(int, x);
+  const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16));
+  const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32));
+  const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48));
+  const int row = lane >> 4;
+  const float above = row == 0 ? t1 + (t2 + t3) : (row == 1 ? t2 + t3 : (row == 2 ? t3 : 0.f));
+  return x + above;
+}
+
 template <int K, int V>
 __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -600,8 +629,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       *reinterpret_cast<f32x4*>(&RowP[hf][3][row0]) = dba;
       *reinterpret_cast<f32x4*>(&RowP[hf][4][row0]) = xr;
     }
-#pragma unroll
-    for (int sh = 1; sh < 64; sh *= 2) sde += __shfl_xor(sde, sh);
+    sde = wave_sum(sde);
     if (lane == 0) Red[w8] = sde;
     __syncthreads();   // ColP, RowP, Red complete
     if (w8 == 0) {
@@ -615,9 +643,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       const float rktw = RowP[0][2][i] + RowP[1][2][i];
       const float rdba = RowP[0][3][i] + RowP[1][3][i];
       const float rxr = RowP[0][4][i] + RowP[1][4][i];
-      float rho_all = rrho;
-#pragma unroll
-      for (int sh = 1; sh < 64; sh *= 2) rho_all += __shfl_xor(rho_all, sh);
+      const float rho_all = wave_sum(rrho);
       float csum = 0.f, cvsum = 0.f;
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
@@ -628,16 +654,9 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       float dG = egi * rq1 - rrho + bi * egi * rktw + rxr - csum;
       if (i == L - 1) dG += __expf(GL) * sd + rho_all;
       if (i < L) dbeta[(size_t)(t0 + i) * Hv + h] = cvsum + egi * rktw + rdba;
-      float x = i < L ? dG : 0.f;
-      // reverse inclusive scan over the 64 rows
-      x = __shfl(x, 63 - lane);
-#pragma unroll
-      for (int d = 1; d < 64; d *= 2) {
-        const float o = __shfl_up(x, d);
-        if (lane >= d) x += o;
-      }
-      const int ir = 63 - lane;
-      if (ir < L) dg[(size_t)(t0 + ir) * Hv + h] = x;
+      // dg = reverse inclusive cumsum of dG over the 64 rows
+      const float x = suffix_sum(i < L ? dG : 0.f, lane);
+      if (i < L) dg[(size_t)(t0 + i) * Hv + h] = x;
     }
     __syncthreads();   // LDS reuse by the next v-head
   };
