@@ -425,10 +425,14 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
       if (sl < NSS) {
         const int ct = 2 * sl + hf;
+        // Q, K at this lane's OL rows row0 + r, column 16 ct + r16: one
+        // transposing read of the group's 4 x 16 block each
+        const u16x4 q4v = lds_tr16(&Qs[row0 + (r16 >> 2)][16 * ct + 4 * (r16 & 3)]);
+        const u16x4 k4v = lds_tr16(&Ks[row0 + (r16 >> 2)][16 * ct + 4 * (r16 & 3)]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float qv = bf2f(Qs[row0 + r][16 * ct + r16]);
-          const float kv = bf2f(Ks[row0 + r][16 * ct + r16]);
+          const float qv = bf2f(q4v[r]);
+          const float kv = bf2f(k4v[r]);
           const float a = scale * x0[r];
           dQa[sl][r] += eg[r] * a;
           qr1[r] += qv * a;
@@ -488,11 +492,12 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
 #pragma unroll
         for (int b = 0; b < 2; ++b)
           tw = mfma16(ta[b], lds_colfrag(&R2s[0][0], LK, 32 * b, 16 * ct, lane), tw);
+        const u16x4 k4v = lds_tr16(&Ks[row0 + (r16 >> 2)][16 * ct + 4 * (r16 & 3)]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float x = -tw[r];   // (T^T dW)
           dKa[m][r] += bt[r] * eg[r] * x;
-          ktw[r] += bf2f(Ks[row0 + r][16 * ct + r16]) * x;
+          ktw[r] += bf2f(k4v[r]) * x;
         }
       }
     }
