@@ -142,9 +142,13 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   __shared__ __attribute__((aligned(16))) unsigned char regA[kRegA];
   __shared__ __attribute__((aligned(16))) unsigned char regB[kRegB];
   uint16_t (*dds)[LV] = reinterpret_cast<uint16_t (*)[LV]>(regA);
-  uint16_t (*R2s)[LK] = reinterpret_cast<uint16_t (*)[LK]>(regB);
-  uint16_t (*Ms)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regB);
-  uint16_t (*MPs)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regA);
+  // R2, M and MP are kept transposed (row = column of the matrix), so that a
+  // lane's four output-layout values (4 rows, one column) are one 8-byte write
+  constexpr int LR = 68;   // row stride of R2^T (K rows of 64 tokens)
+  static_assert(K * LR * 2 <= kRegB, "R2^T must fit in regB");
+  uint16_t (*R2t)[LR] = reinterpret_cast<uint16_t (*)[LR]>(regB);
+  uint16_t (*Mt)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regB);
+  uint16_t (*MPt)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regA);
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
   // column partial sums over 8-row parts: of X (0) and of T * (dd V^T) (1)
@@ -439,8 +443,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
           const float d2 = dec[r] * x2[r];
           dKa[sl][r] += d2;
           rho[r] += kv * d2;
-          R2s[row0 + r][16 * ct + r16] = f2bf(x1[r]);
         }
+        *reinterpret_cast<u16x4*>(&R2t[16 * ct + r16][row0]) = f2bf4(x1);
       } else {
         dpt[sl - NSS] = x0;
         ddv[sl - NSS] = x1;
@@ -452,7 +456,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     {
       u16x8 a2[KB];
 #pragma unroll
-      for (int b = 0; b < KB; ++b) a2[b] = *reinterpret_cast<const u16x8*>(&R2s[rowA][32 * b + 8 * grp]);
+      for (int b = 0; b < KB; ++b) a2[b] = lds_colfrag(&R2t[0][0], LR, 32 * b, 16 * rt, lane);
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const int ct = 2 * m + hf;
@@ -491,7 +495,9 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         f32x4 tw = zero4();
 #pragma unroll
         for (int b = 0; b < 2; ++b)
-          tw = mfma16(ta[b], lds_colfrag(&R2s[0][0], LK, 32 * b, 16 * ct, lane), tw);
+          tw = mfma16(ta[b], cat8(*reinterpret_cast<const u16x4*>(&R2t[16 * ct + r16][32 * b + 8 * grp]),
+                                  *reinterpret_cast<const u16x4*>(&R2t[16 * ct + r16][32 * b + 8 * grp + 4])),
+                      tw);
         const u16x4 k4v = lds_tr16(&Ks[row0 + (r16 >> 2)][16 * ct + 4 * (r16 & 3)]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -558,20 +564,23 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     for (int m = 0; m < 2; ++m) {
       const int j = 16 * (2 * m + hf) + r16;
       const float Gj = Gs[j];
+      f32x4 mv, mpv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = row0 + r;
         const float gam = (j <= i) ? __expf(Gs[i] - Gj) : 0.f;
         const float dA = (j < i) ? -da[m][r] : 0.f;
         const float dP = (j <= i) ? scale * dpt[m][r] : 0.f;
-        Ms[i][j] = f2bf(dA * bt[r] * gam);
-        MPs[i][j] = f2bf(dP * gam);
+        mv[r] = dA * bt[r] * gam;
+        mpv[r] = dP * gam;
         dba[r] += dA * kk[m][r] * gam;
         const float x = (dA * bt[r] * kk[m][r] + dP * qk[m][r]) * gam;
         xr[r] += x;
         X32[i][j] = x;
         T32[i][j] *= ddv[m][r];   // T_ij (dd V^T)_ij, summed over i for column j below
       }
+      *reinterpret_cast<u16x4*>(&Mt[j][row0]) = f2bf4(mv);
+      *reinterpret_cast<u16x4*>(&MPt[j][row0]) = f2bf4(mpv);
     }
     __syncthreads();
     {
@@ -594,10 +603,10 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       u16x8 am[2], amt[2], ap[2], apt[2];
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        am[b] = *reinterpret_cast<const u16x8*>(&Ms[rowA][32 * b + 8 * grp]);
-        ap[b] = *reinterpret_cast<const u16x8*>(&MPs[rowA][32 * b + 8 * grp]);
-        amt[b] = lds_colfrag(&Ms[0][0], LC, 32 * b, 16 * rt, lane);
-        apt[b] = lds_colfrag(&MPs[0][0], LC, 32 * b, 16 * rt, lane);
+        am[b] = lds_colfrag(&Mt[0][0], LC, 32 * b, 16 * rt, lane);
+        ap[b] = lds_colfrag(&MPt[0][0], LC, 32 * b, 16 * rt, lane);
+        amt[b] = *reinterpret_cast<const u16x8*>(&Mt[rowA][32 * b + 8 * grp]);
+        apt[b] = *reinterpret_cast<const u16x8*>(&MPt[rowA][32 * b + 8 * grp]);
       }
 #pragma unroll
       for (int m = 0; m < KH; ++m) {
