@@ -151,8 +151,9 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   uint16_t (*MPt)[LC] = reinterpret_cast<uint16_t (*)[LC]>(regA);
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
-  // column partial sums over 8-row parts: of X (0) and of T * (dd V^T) (1)
-  __shared__ __attribute__((aligned(16))) float ColP[2][8][64];
+  // column partial sums over each row tile's 16 rows: of X (0) and of
+  // T * (dd V^T) (1)
+  __shared__ __attribute__((aligned(16))) float ColP[2][4][64];
   __shared__ __attribute__((aligned(16))) float RowP[2][5][64];   // row partials per half
   __shared__ float Red[8];
 
@@ -534,7 +535,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
           da[m] = mfma4f32(T32[j0 + grp][rowA], X32[j0 + grp][16 * ct + r16], da[m]);
       }
     }
-    __syncthreads();   // X32 (M1) reads done before X is written there
+    // (no barrier here: the phases up to the next one write only Mt / MPt
+    // (regB / regA, free since the T^T products) and ColP)
 
     // ---- K K^T and Q K^T (OL, this wave's two column tiles)
     f32x4 kk[2], qk[2];
@@ -558,13 +560,14 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         }
       }
     }
-    // ---- C x C elementwise: M, MP, dbeta / dG terms, X; T * (dd V^T) for the column sums
+    // ---- C x C elementwise: M, MP, dbeta / dG terms, the column sums of X and T * (dd V^T)
     f32x4 dba = zero4(), xr = zero4();
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int j = 16 * (2 * m + hf) + r16;
       const float Gj = Gs[j];
       f32x4 mv, mpv;
+      float xc = 0.f, tc = 0.f;   // column j over this lane's 4 rows
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = row0 + r;
@@ -576,25 +579,23 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         dba[r] += dA * kk[m][r] * gam;
         const float x = (dA * bt[r] * kk[m][r] + dP * qk[m][r]) * gam;
         xr[r] += x;
-        X32[i][j] = x;
-        T32[i][j] *= ddv[m][r];   // T_ij (dd V^T)_ij, summed over i for column j below
+        xc += x;
+        tc += T32[i][j] * ddv[m][r];   // T_ij (dd V^T)_ij
       }
       *reinterpret_cast<u16x4*>(&Mt[j][row0]) = f2bf4(mv);
       *reinterpret_cast<u16x4*>(&MPt[j][row0]) = f2bf4(mpv);
-    }
-    __syncthreads();
-    {
-      // every thread: column tid % 64 over the 8 rows of part tid / 64
-      const int col = tid & 63, part = tid >> 6;
-      float c = 0.f, cv = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        c += X32[8 * part + i][col];
-        cv += T32[8 * part + i][col];
+      // over the row tile's 16 rows (the wave's 4 lane groups): one partial
+      // per (row tile, column)
+      xc += __shfl_xor(xc, 16);
+      xc += __shfl_xor(xc, 32);
+      tc += __shfl_xor(tc, 16);
+      tc += __shfl_xor(tc, 32);
+      if (grp == 0) {
+        ColP[0][rt][j] = xc;
+        ColP[1][rt][j] = tc;
       }
-      ColP[0][part][col] = c;
-      ColP[1][part][col] = cv;
     }
+    __syncthreads();   // M, MP complete
 
     if constexpr (decltype(prefetch_next)::value) issue_stage(gi + 1);
 
@@ -660,7 +661,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       const float rho_all = wave_sum(rrho);
       float csum = 0.f, cvsum = 0.f;
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
+      for (int x = 0; x < 4; ++x) {
         csum += ColP[0][x][i];
         cvsum += ColP[1][x][i];
       }
