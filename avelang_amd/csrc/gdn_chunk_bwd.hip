@@ -510,20 +510,27 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     }
     __syncthreads();   // X32 = dT complete; dd / R2 no longer needed
 
-    // ---- dA = strict_lower(-T^T (dT T^T)) on fp32 MFMA (T lower triangular)
+    // ---- dA = strict_lower(-T^T (dT T^T)) on fp32 MFMA (T lower triangular).
+    // In step s of a 16-deep block q, lane (r16, grp) supplies k = 16 q +
+    // 4 grp + s, so its four A or B values of a block are one float4 of a row.
     f32x4 m1[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int ct = 2 * m + hf;
       m1[m] = zero4();
-      for (int j0 = 0; j0 < 16 * (ct + 1); j0 += 4)
-        m1[m] = mfma4f32(X32[rowA][j0 + grp], T32[16 * ct + r16][j0 + grp], m1[m]);
+      for (int q = 0; q <= ct; ++q) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&X32[rowA][16 * q + 4 * grp]);
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&T32[16 * ct + r16][16 * q + 4 * grp]);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) m1[m] = mfma4f32(a4[st], b4[st], m1[m]);
+      }
     }
     __syncthreads();
+    // M1 goes back transposed (X32 then holds M1^T): a lane's 4 output-layout
+    // rows of column 16 ct + r16 are one float4
 #pragma unroll
     for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) X32[row0 + r][16 * (2 * m + hf) + r16] = m1[m][r];
+      *reinterpret_cast<f32x4*>(&X32[16 * (2 * m + hf) + r16][row0]) = m1[m];
     __syncthreads();
     f32x4 da[2];
 #pragma unroll
@@ -531,8 +538,13 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       const int ct = 2 * m + hf;
       da[m] = zero4();
       if (ct <= rt) {
-        for (int j0 = 16 * rt; j0 < 64; j0 += 4)
-          da[m] = mfma4f32(T32[j0 + grp][rowA], X32[j0 + grp][16 * ct + r16], da[m]);
+        for (int q = rt; q < 4; ++q) {
+          // B[k][n] = M1[k][16 ct + n] = M1^T[16 ct + n][k]
+          const f32x4 b4 = *reinterpret_cast<const f32x4*>(&X32[16 * ct + r16][16 * q + 4 * grp]);
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            da[m] = mfma4f32(T32[16 * q + 4 * grp + st][rowA], b4[st], da[m]);
+        }
       }
     }
     // (no barrier here: the phases up to the next one write only Mt / MPt
