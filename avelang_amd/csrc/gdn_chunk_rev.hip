@@ -404,17 +404,23 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         const int t0 = s + jc * kChunk, L = live ? min(kChunk, e - t0) : 0;
         const int b3 = j % 3;
         const size_t ci = live ? (size_t)(c_begin + jc) : 0;
+        // store i, lane l: row 16 vt + rpi i + l / cpr, columns 8 (l % cpr)
+        // .. + 7, i.e. rpi whole rows per store (fragment lane r16 + 16 grp
+        // of k-block b holds row r16, columns 32 b + 8 grp .. + 7)
+        constexpr int cpr = K / 8, rpi = 64 / cpr;
+        const int c8 = lane % cpr;
         u16x8 sh[KB];
         if (live) {
 #pragma unroll
-          for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][b][lane];
+          for (int i = 0; i < KB; ++i) sh[i] = Sx[b3][c8 >> 2][(rpi * i + lane / cpr) + 16 * (c8 & 3)];
         }
         const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
             dse + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
 #pragma unroll
-        for (int b = 0; b < KB; ++b)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, sh[b]), hr,
-                                                 ((16 * vt + r16) * K + 32 * b + 8 * grp) * 2, 0, 0);
+        for (int i = 0; i < KB; ++i)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, sh[i]), hr,
+                                                 ((16 * vt + rpi * i + lane / cpr) * K + 8 * c8) * 2,
+                                                 0, 0);
         // lane t gathers token row t of dd from the fragments in LDS (element
         // t % 8 of fragment lane 16 ((t / 8) % 4) + n of k-block t / 32)
         const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
