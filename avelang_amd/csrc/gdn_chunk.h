@@ -19,7 +19,9 @@ struct ChunkWs {
   uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] (use_qk_l2norm only),
   uint16_t* kn;     // written by the prep kernel, read by the chain
   // backward only
-  float* tmat;      // [NC][Hv][64][64] T = (I + A)^-1 (fp32, row-major, upper part 0)
+  float* tmat;      // [NC][Hv][10][16][16] T = (I + A)^-1 (fp32): its lower 16 x 16
+                    // blocks (rt, cb), cb <= rt, in the order tmat_block() gives,
+                    // each row-major (the diagonal blocks' upper part 0)
   u16x8* ttfrag;    // [NC][Hv][4][2][2][64] A-operand fragments of Tb^T (hi, lo)
   u16x8* ptfrag;    // [NC][Hv][4][2][64]    A-operand fragments of P^T
   u16x8* qtfrag;    // [NC][Hqk][K/16][2][64] A-operand fragments of Q^T (key-row tile,
@@ -27,6 +29,16 @@ struct ChunkWs {
   uint16_t* hs;     // [NC][Hv][V][K] bf16: state at the start of every chunk, transposed
   uint16_t* dl;     // [B*T][Hv][V]   bf16: d = vnew, the per-token delta
 };
+
+// Packed T: the 10 lower 16 x 16 blocks of the 64 x 64 matrix, block
+// (rt, cb) at index rt (rt + 1) / 2 + cb; the upper blocks are zero and not
+// stored.
+constexpr int kTBlocks = 10;
+constexpr int kTPacked = kTBlocks * 256;   // floats per (chunk, v-head)
+__host__ __device__ constexpr int tmat_block(int rt, int cb) { return rt * (rt + 1) / 2 + cb; }
+__host__ __device__ constexpr int tmat_block_row(int bi) {
+  return bi >= 6 ? 3 : (bi >= 3 ? 2 : (bi >= 1 ? 1 : 0));
+}
 
 __device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int total,
                                            int& s, int& e) {

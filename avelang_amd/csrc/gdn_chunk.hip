@@ -146,10 +146,12 @@ __device__ __forceinline__ void scale_frags(u16x8 (&f)[KB], float r) {
 
 // One workgroup per (chunk, v-head).  Wave w owns chunk rows 16w..16w+15.
 // BWD (the backward's recomputation) also writes T itself and the A-operand
-// fragments of Tb^T and P^T for the reverse chain.  L2: use_qk_l2norm (a
-// compile-time flag: with one code path per form the compiler's waits for
-// the K / Q row loads never include the normalised rows' stores).
-template <int K, bool BWD, bool L2>
+// fragments of Tb^T and P^T for the reverse chain.  OUT: the chain forms the
+// output, and so reads the P fragments (the backward's recomputation does
+// not).  L2: use_qk_l2norm (a compile-time flag: with one code path per form
+// the compiler's waits for the K / Q row loads never include the normalised
+// rows' stores).
+template <int K, bool BWD, bool OUT, bool L2>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ g, const float* __restrict__ beta,
@@ -328,7 +330,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     // P fragment slot: k-block tc/2, fragment lane r16 + 16 (2 (tc%2) + grp/2),
     // elements 4 (grp%2) .. +3
     // (k-block 1 of row tiles 0 and 1 is zero and never read: not stored)
-    if (tc < 2 || w >= 2) {
+    if (OUT && (tc < 2 || w >= 2)) {
       const size_t pf = (pbase + tc / 2) * 64 + r16 + 16 * (2 * (tc % 2) + grp / 2);
       *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(ws.pfrag + pf) + 4 * (grp % 2)) =
           __builtin_bit_cast(u32x2, pv);
@@ -453,16 +455,14 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       // P^T fragments: P^T[m][kk] = P[kk][m]
       ws.ptfrag[(base * 2 + b) * 64 + lane] = lds_colfrag(&Ps[0][0], 72, 32 * b, 16 * w, lane);
     }
-    // T itself, row-major fp32 with the (unwritten) upper blocks as zero
-    float* tdst = ws.tmat + ((size_t)ci * Hv + h) * 64 * 64;
-    const int tr = tid / 4, tc0 = 16 * (tid % 4);
-#pragma unroll
-    for (int c4 = 0; c4 < 16; c4 += 4) {
-      f32x4 x;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = (tc0 + c4 + r <= tr) ? Tm[tr * kLdA + tc0 + c4 + r] : 0.f;
-      *reinterpret_cast<f32x4*>(tdst + tr * 64 + tc0 + c4) = x;
-    }
+    // T itself, fp32, its lower blocks only: wave w stores blocks (w, 0..w)
+    // of its row tile, one contiguous 1 KB block per store (the diagonal
+    // block's upper part is zero in Tm)
+    float* tdst = ws.tmat + ((size_t)ci * Hv + h) * kTPacked;
+    const int tr = 16 * w + lane / 4, tc4 = 4 * (lane % 4);
+    for (int cb = 0; cb <= w; ++cb)
+      *reinterpret_cast<f32x4*>(tdst + 256 * tmat_block(w, cb) + 4 * lane) =
+          *reinterpret_cast<const f32x4*>(&Tm[tr * kLdA + 16 * cb + tc4]);
   }
 }
 
@@ -492,7 +492,7 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
     p.kn = take((size_t)total * Hqk * K * 2);
   }
   if (bwd) {
-    p.tmat = take(nch * 64 * 64 * 4);
+    p.tmat = take(nch * kTPacked * 4);
     p.ttfrag = take(nch * 4 * 2 * 2 * 64 * 16);
     p.ptfrag = take(nch * 4 * 2 * 64 * 16);
     p.hs = take(nch * K * V * 2);
@@ -538,10 +538,10 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
                        (int)p.ncmax, ws.off, ws.status);
   if (p.ncmax > 0) {
     if (l2)
-      hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, true>), dim3((unsigned)p.ncmax, Hv), dim3(256),
+      hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, OUT, true>), dim3((unsigned)p.ncmax, Hv), dim3(256),
                          0, st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws, gate);
     else
-      hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, false>), dim3((unsigned)p.ncmax, Hv), dim3(256),
+      hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, OUT, false>), dim3((unsigned)p.ncmax, Hv), dim3(256),
                          0, st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws, gate);
   }
   // with use_qk_l2norm the chain reads the rows the prep kernel normalised

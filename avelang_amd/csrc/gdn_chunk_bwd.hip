@@ -210,6 +210,16 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       *reinterpret_cast<u16x8*>(&Qs[r][c8]) = qr[i];
     }
   }
+  // the upper 16 x 16 blocks of T (zero, not stored in the workspace): set
+  // once here, the v-heads write only the lower blocks
+#pragma unroll
+  for (int i = 0; i < 64 * 16 / NTH; ++i) {
+    const int idx = tid + NTH * i, r = idx / 16, c4 = 4 * (idx % 16);
+    if (c4 / 16 > r / 16) {
+      *reinterpret_cast<f32x4*>(&T32[r][c4]) = zero4();
+      *reinterpret_cast<u16x4*>(&Tb16[r][c4]) = u16x4{0, 0, 0, 0};
+    }
+  }
   __syncthreads();
 
   f32x4 dQa[KH], dKa[KH];   // column tiles 2m + hf
@@ -225,7 +235,10 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   // into registers: for the first v-head here, for each later one before the
   // previous v-head's dK / dQ products, so their latency overlaps that
   // v-head's last phases instead of opening the next one.
-  constexpr int NT = 64 * 16 / NTH, ND = 64 * V / 8 / NTH;
+  // T arrives as its 10 lower 16 x 16 blocks (1 KB each): wave w loads block
+  // w, waves 0 and 1 also blocks 8 and 9
+  static_assert(NTH == 512 && kTBlocks == 10, "one T block per wave, two more for waves 0, 1");
+  constexpr int NT = 2, ND = 64 * V / 8 / NTH;
   u16x8 pre[3][2];
   f32x4 tv[NT];
   u16x8 dv8[ND];
@@ -249,7 +262,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const __amdgpu_buffer_rsrc_t rE = __builtin_amdgcn_make_buffer_rsrc(
         ws.dse + ch * K * V, 0, K * V * 2, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rT = __builtin_amdgcn_make_buffer_rsrc(
-        ws.f.tmat + ch * 64 * 64, 0, 64 * 64 * 4, kBufferFlags);
+        ws.f.tmat + ch * kTPacked, 0, kTPacked * 4, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdd = __builtin_amdgcn_make_buffer_rsrc(
         ws.dd + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
@@ -272,9 +285,12 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < NT; ++i)
-      tv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rT, 16 * tid, 16 * NTH * i, 0));
+    {
+      const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+      tv[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rT, 16 * lane, 1024 * w, 0));
+      if (w < 2)
+        tv[1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rT, 16 * lane, 1024 * (8 + w), 0));
+    }
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
       const int idx = tid + NTH * i, r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
@@ -373,9 +389,13 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     store_slice(0, pre[0]);
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
-      const int idx = tid + NTH * i, r = idx / 16, c4 = 4 * (idx % 16);
-      *reinterpret_cast<f32x4*>(&T32[r][c4]) = tv[i];
-      *reinterpret_cast<u16x4*>(&Tb16[r][c4]) = f2bf4(tv[i]);
+      if (i == 0 || w8 < 2) {
+        const int bi = i == 0 ? w8 : 8 + w8;
+        const int brt = tmat_block_row(bi), bcb = bi - tmat_block(brt, 0);
+        const int r = 16 * brt + lane / 4, c4 = 16 * bcb + 4 * (lane % 4);
+        *reinterpret_cast<f32x4*>(&T32[r][c4]) = tv[i];
+        *reinterpret_cast<u16x4*>(&Tb16[r][c4]) = f2bf4(tv[i]);
+      }
     }
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
