@@ -15,7 +15,7 @@ struct ChunkWs {
   int32_t* status;  // [1] 0, or the cu_seqlens violation the chunk table found
   float* gate;      // [NC][Hv][64]: G_i, the chunk-local cumulative log-decay
   u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
-  u16x8* pfrag;     // [NC][Hv][4][2][64]
+  u16x8* pfrag;     // [NC][Hv][4][2][64] (not written by the backward's recomputation)
   uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] (use_qk_l2norm only),
   uint16_t* kn;     // written by the prep kernel, read by the chain
   // backward only
@@ -24,6 +24,7 @@ struct ChunkWs {
                     // each row-major (the diagonal blocks' upper part 0)
   u16x8* ttfrag;    // [NC][Hv][4][2][2][64] A-operand fragments of Tb^T (hi, lo)
   u16x8* ptfrag;    // [NC][Hv][4][2][64]    A-operand fragments of P^T
+                    // (both: row tiles 2, 3 of k-block 0 are zero and left unwritten)
   u16x8* qtfrag;    // [NC][Hqk][K/16][2][64] A-operand fragments of Q^T (key-row tile,
                     // token k-block; the l2-normalised q with use_qk_l2norm)
   uint16_t* hs;     // [NC][Hv][V][K] bf16: state at the start of every chunk, transposed

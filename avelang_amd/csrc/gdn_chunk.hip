@@ -435,11 +435,14 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
   }
   if constexpr (BWD) {
-    // Tb^T fragments, row tile w: Tb^T[m][kk] = T[kk][m] beta_m (kk >= m)
+    // Tb^T fragments, row tile w: Tb^T[m][kk] = T[kk][m] beta_m (kk >= m);
+    // k-block 0 of row tiles 2 and 3 is zero (in Tb^T and P^T) and never
+    // read: not stored
     const int m = 16 * w + r16;
     const float bm = Bs[m];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
+      if (b == 0 && w >= 2) continue;
       u16x8 th, tl;
 #pragma unroll
       for (int ii = 0; ii < 8; ++ii) {

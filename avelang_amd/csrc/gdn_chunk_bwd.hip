@@ -342,14 +342,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         ws.f.hs + ch * K * V, 0, K * V * 2, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rE = __builtin_amdgcn_make_buffer_rsrc(
         ws.dse + ch * K * V, 0, K * V * 2, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rT = __builtin_amdgcn_make_buffer_rsrc(
-        ws.f.tmat + ch * 64 * 64, 0, 64 * 64 * 4, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rdd = __builtin_amdgcn_make_buffer_rsrc(
-        ws.dd + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
         ws.f.dl + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
 
@@ -379,8 +373,18 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         *reinterpret_cast<u16x8*>(&Stg[sl & 1][1][sp_r][sp_c8]) = buf[1];
       }
       if (sl < NSS) {
+        // bf16 pairs straight into v_dot2_f32_bf16.  Each pair passes an
+        // empty asm statement of its own: bound as whole vectors instead,
+        // this compiler fed the first pair's registers to all four products.
+        const u32x4 a = __builtin_bit_cast(u32x4, buf[0]), b = __builtin_bit_cast(u32x4, buf[1]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sde += bf2f(buf[0][j]) * bf2f(buf[1][j]);
+        for (int j = 0; j < 4; ++j) {
+          unsigned int aj = a[j], bj = b[j];
+          asm("" : "+v"(aj));
+          asm("" : "+v"(bj));
+          sde = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, aj),
+                                                __builtin_bit_cast(bf16x2, bj), sde, false);
+        }
       }
     };
 

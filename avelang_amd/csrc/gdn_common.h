@@ -46,6 +46,7 @@ __device__ __forceinline__ void split_bf(float x, uint16_t& hi, uint16_t& lo) {
 // part re-expanded from the packed words with a shift / mask): the same
 // results as f2bf / split_bf per element, in fewer instructions.
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x2p __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u16x4 f2bf4(f32x4 x) {
   return __builtin_bit_cast(u16x4, __builtin_convertvector(x, bf16x4));
