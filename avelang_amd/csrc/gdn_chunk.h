@@ -41,6 +41,21 @@ __host__ __device__ constexpr int tmat_block_row(int bi) {
   return bi >= 6 ? 3 : (bi >= 3 ? 2 : (bi >= 1 ? 1 : 0));
 }
 
+// Compute units of the current device, looked up once per device.
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
 __device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int total,
                                            int& s, int& e) {
   if (cu) {

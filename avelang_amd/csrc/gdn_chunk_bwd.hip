@@ -21,9 +21,11 @@
 //                       sequence's chunks; dS' in one wave's VGPRs (fp32),
 //                       hi+lo splits where a product feeds dS (as the forward
 //                       chain); stores dS' of every chunk and dd (bf16) and dh0
-//   chunk_grad_kernel   one workgroup per (chunk, qk-head), fully parallel:
-//                       the local gradients of the group's v-heads, dq / dk
-//                       summed over the group in registers
+//   chunk_grad_kernel   one resident workgroup per CU, taking (chunk,
+//                       qk-head) items in turn, fully parallel: the local
+//                       gradients of the group's v-heads, dq / dk summed over
+//                       the group in registers
+#include <algorithm>
 #include <type_traits>
 
 #include "gdn_chunk.h"
@@ -37,7 +39,8 @@ struct BwdWs {
 };
 
 // --------------------------------------------------- gradient kernel ----
-// One workgroup of 8 waves per (chunk, qk-head).  Wave w8 owns row tile
+// A workgroup of 8 waves works on one (chunk, qk-head) item at a time.
+// Wave w8 owns row tile
 // rt = w8 % 4 (chunk rows 16rt..16rt+15) and the column tiles of parity
 // hf = w8 / 4 of every [64 x *] result.  "OL" = the MFMA output layout:
 // lane (r16, grp) holds rows 16rt + 4grp + r (r = 0..3) of column 16ct + r16.
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const uint16_t* __restrict__ qraw, const uint16_t* __restrict__ kraw,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dO,
     const float* __restrict__ beta, const int32_t* __restrict__ cu, int N, int T, int total,
-    int Hqk, int Hv, float scale, int l2norm, BwdWs ws, uint16_t* __restrict__ dq,
+    int Hqk, int Hv, int nchunks, float scale, int l2norm, BwdWs ws, uint16_t* __restrict__ dq,
     uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, float* __restrict__ dg,
     float* __restrict__ dbeta) {
   constexpr int NTH = kGradThreads;
@@ -157,44 +160,65 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   __shared__ __attribute__((aligned(16))) float RowP[2][5][64];   // row partials per half
   __shared__ float Red[8];
 
-  const int ci = blockIdx.x;
-  const int hq = blockIdx.y;
-  int n, cfirst;
-  if (cu) {
-    const int32_t* off = ws.f.off;
-    if (ci >= off[N]) return;
-    int lo = 0, hi = N;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (off[mid] <= ci) lo = mid; else hi = mid;
-    }
-    n = lo;
-    cfirst = off[n];
-  } else {
-    const int nct = (T + kChunk - 1) / kChunk;
-    n = ci / nct;
-    cfirst = n * nct;
-  }
-  int s, e;
-  seq_bounds(cu, n, T, total, s, e);
-  const int t0 = s + (ci - cfirst) * kChunk;
-  const int L = min(kChunk, e - t0);
   const int Gn = Hv / Hqk;
+  const int tid = threadIdx.x;
 
-  const int tid = threadIdx.x, lane = tid % 64;
-  const int w8 = __builtin_amdgcn_readfirstlane(tid / 64);   // wave index (scalar)
-  const int rt = w8 & 3, hf = w8 >> 2;
-  const int r16 = lane % 16, grp = lane / 16;
-  const int row0 = 16 * rt + 4 * grp;     // first OL row of this lane
+  // Work items (chunk, qk-head): item x is chunk x % nchunks of qk-head
+  // x / nchunks, and a workgroup takes items x = blockIdx.x + j gridDim.x, so
+  // that it stays resident and requests its next item's first operands
+  // during the current item's last v-head.  A varlen item past the last
+  // chunk is empty and skipped.
+  struct Item {
+    int ci, hq, t0, L;
+  };
+  const int nitems = nchunks * Hqk;
+  auto find_item = [&](int& x, Item& it) -> bool {
+    for (; x < nitems; x += gridDim.x) {
+      const int ci = x % nchunks;
+      int n, cfirst;
+      if (cu) {
+        const int32_t* off = ws.f.off;
+        if (ci >= off[N]) continue;
+        int lo = 0, hi = N;
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (off[mid] <= ci) lo = mid; else hi = mid;
+        }
+        n = lo;
+        cfirst = off[n];
+      } else {
+        const int nct = (T + kChunk - 1) / kChunk;
+        n = ci / nct;
+        cfirst = n * nct;
+      }
+      int s, e;
+      seq_bounds(cu, n, T, total, s, e);
+      it.ci = ci;
+      it.hq = x / nchunks;
+      it.t0 = s + (ci - cfirst) * kChunk;
+      it.L = min(kChunk, e - it.t0);
+      return true;
+    }
+    return false;
+  };
+  int x = blockIdx.x;
+  Item cur;
+  if (!find_item(x, cur)) return;
+  // the item being worked on (read by the v-head body and the dq / dk stores)
+  int ci = cur.ci, hq = cur.hq, t0 = cur.t0, L = cur.L;
+  int qkbytes = 0, vbytes = 0;
 
-  // K / Q rows of the chunk (rows >= L read as zero)
-  const int qkbytes = L * Hqk * K * 2;
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(k + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(q + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
-  {
-    constexpr int NQ = 64 * K / 8 / NTH;   // 16-byte chunks per thread
+  // K / Q rows of an item's chunk (rows >= L read as zero) into Ks / Qs,
+  // through registers that live only here
+  constexpr int NQ = 64 * K / 8 / NTH;   // 16-byte chunks per thread
+  auto stage_kq = [&](const Item& it) {
+    int tid = threadIdx.x;   // (re-formed per call: see the v-head body)
+    asm volatile("" : "+v"(tid));
+    const int nb = it.L * Hqk * K * 2;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(k + ((size_t)it.t0 * Hqk + it.hq) * K), 0, nb, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(q + ((size_t)it.t0 * Hqk + it.hq) * K), 0, nb, kBufferFlags);
     u16x8 kr[NQ], qr[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
@@ -209,7 +233,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       *reinterpret_cast<u16x8*>(&Ks[r][c8]) = kr[i];
       *reinterpret_cast<u16x8*>(&Qs[r][c8]) = qr[i];
     }
-  }
+  };
   // the upper 16 x 16 blocks of T (zero, not stored in the workspace): set
   // once here, the v-heads write only the lower blocks
 #pragma unroll
@@ -220,21 +244,16 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       *reinterpret_cast<u16x4*>(&Tb16[r][c4]) = u16x4{0, 0, 0, 0};
     }
   }
-  __syncthreads();
 
   f32x4 dQa[KH], dKa[KH];   // column tiles 2m + hf
-#pragma unroll
-  for (int m = 0; m < KH; ++m) {
-    dQa[m] = zero4();
-    dKa[m] = zero4();
-  }
 
-  const int vbytes = L * Hv * V * 2;
   // Operands of a v-head's staging phase (slices 0..2 of S / dS' or d / V,
   // T, the dd rows, G and beta, the A fragments of dO / dd / d), requested
-  // into registers: for the first v-head here, for each later one before the
-  // previous v-head's dK / dQ products, so their latency overlaps that
-  // v-head's last phases instead of opening the next one.
+  // into registers: for the first item's first v-head before the loop, for
+  // every later v-head (of this item or the next) before the previous
+  // v-head's dK / dQ products, so their latency overlaps that v-head's last
+  // phases instead of opening the next one.  live = false (no next item)
+  // requests them from empty resources.
   // T arrives as its 10 lower 16 x 16 blocks (1 KB each): wave w loads block
   // w, waves 0 and 1 also blocks 8 and 9
   static_assert(NTH == 512 && kTBlocks == 10, "one T block per wave, two more for waves 0, 1");
@@ -244,9 +263,11 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   u16x8 dv8[ND];
   u16x8 aO[VB], aD[VB], aL[VB];
   float gsv = 0.f, bsv = 0.f;
-  auto issue_stage = [&](int gi_t) {
+  auto issue_stage = [&](const Item& it, int gi_t, bool live) {
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
+    const int ci = it.ci, t0 = it.t0, L = it.L, hq = it.hq;
+    const int vbytes = live ? L * Hv * V * 2 : 0;
     const int lane = tid % 64;
     const int rt = __builtin_amdgcn_readfirstlane(tid / 64) & 3;
     const int r16 = lane % 16, grp = lane / 16;
@@ -258,11 +279,11 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const int h = hq * Gn + gi_t;
     const size_t ch = (size_t)ci * Hv + h;
     const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
-        ws.f.hs + ch * K * V, 0, K * V * 2, kBufferFlags);
+        ws.f.hs + ch * K * V, 0, live ? K * V * 2 : 0, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rE = __builtin_amdgcn_make_buffer_rsrc(
-        ws.dse + ch * K * V, 0, K * V * 2, kBufferFlags);
+        ws.dse + ch * K * V, 0, live ? K * V * 2 : 0, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rT = __builtin_amdgcn_make_buffer_rsrc(
-        ws.f.tmat + ch * kTPacked, 0, kTPacked * 4, kBufferFlags);
+        ws.f.tmat + ch * kTPacked, 0, live ? kTPacked * 4 : 0, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdd = __builtin_amdgcn_make_buffer_rsrc(
         ws.dd + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
@@ -309,12 +330,11 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       aL[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
     }
   };
-  issue_stage(0);
-  // One v-head of the group.  Instantiated with and without the next
-  // v-head's prefetch, so that the prefetch is unconditional where it is
-  // made (a conditional one keeps the previous operands live through the
-  // whole v-head for the path that skips it, which spills).
-  auto vhead = [&](int gi, auto prefetch_next) {
+  // One v-head of the group; prefetch() requests the next v-head's operands
+  // (of this item or the next).  It is made unconditionally: a conditional
+  // one keeps the previous operands live through the whole v-head for the
+  // path that skips it, which spills.
+  auto vhead = [&](int gi, auto prefetch) {
     // The lane index is passed through an empty asm statement once per
     // v-head, so the many per-lane LDS / buffer addresses derived from it are
     // formed inside the loop where they are used, instead of being hoisted
@@ -633,7 +653,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     }
     __syncthreads();   // M, MP complete
 
-    if constexpr (decltype(prefetch_next)::value) issue_stage(gi + 1);
+    prefetch();
 
     // ---- dK += M K + M^T K + MP^T Q,  dQ += MP K (this wave's column tiles)
     {
@@ -711,73 +731,110 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     }
     __syncthreads();   // LDS reuse by the next v-head
   };
-  for (int gi = 0; gi + 1 < Gn; ++gi) vhead(gi, std::true_type{});
-  vhead(Gn - 1, std::false_type{});
-
-  // ---- dq, dk: through the l2norm when the forward normalised q, k
-  const __amdgpu_buffer_rsrc_t rdq = __builtin_amdgcn_make_buffer_rsrc(
-      dq + ((size_t)t0 * Hqk + hq) * K, 0, qkbytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rdk = __builtin_amdgcn_make_buffer_rsrc(
-      dk + ((size_t)t0 * Hqk + hq) * K, 0, qkbytes, kBufferFlags);
-  if (l2norm) {
-    const __amdgpu_buffer_rsrc_t rqr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rkr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(kraw + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
-    f32x4 sq = zero4(), sk = zero4(), pq = zero4(), pk = zero4();
-    float xq[KH][4], xk[KH][4];
+  issue_stage(cur, 0, true);
+  stage_kq(cur);
+  for (;;) {
+    __syncthreads();
+    ci = cur.ci;
+    hq = cur.hq;
+    t0 = cur.t0;
+    L = cur.L;
+    qkbytes = L * Hqk * K * 2;
+    vbytes = L * Hv * V * 2;
 #pragma unroll
     for (int m = 0; m < KH; ++m) {
-      const int ct = 2 * m + hf;
+      dQa[m] = zero4();
+      dKa[m] = zero4();
+    }
+    int xn = x + gridDim.x;
+    Item nxt;
+    const bool more = find_item(xn, nxt);
+    if (!more) nxt = cur;
+    for (int gi = 0; gi + 1 < Gn; ++gi) vhead(gi, [&] { issue_stage(cur, gi + 1, true); });
+    vhead(Gn - 1, [&] { issue_stage(nxt, 0, more); });
+
+    // ---- dq, dk: through the l2norm when the forward normalised q, k
+    // (the lane indices re-formed here, as in the v-head body, so that the
+    // stores' per-lane offsets are not kept live across the item loop)
+    {
+      int tid = threadIdx.x;
+      asm volatile("" : "+v"(tid));
+      const int lane = tid % 64;
+      const int hf = __builtin_amdgcn_readfirstlane(tid / 64) >> 2;
+      const int r16 = lane % 16;
+      const int row0 = 16 * (__builtin_amdgcn_readfirstlane(tid / 64) & 3) + 4 * (lane / 16);
+      const __amdgpu_buffer_rsrc_t rdq = __builtin_amdgcn_make_buffer_rsrc(
+          dq + ((size_t)t0 * Hqk + hq) * K, 0, qkbytes, kBufferFlags);
+      const __amdgpu_buffer_rsrc_t rdk = __builtin_amdgcn_make_buffer_rsrc(
+          dk + ((size_t)t0 * Hqk + hq) * K, 0, qkbytes, kBufferFlags);
+      if (l2norm) {
+        const __amdgpu_buffer_rsrc_t rqr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rkr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(kraw + ((size_t)t0 * Hqk + hq) * K), 0, qkbytes, kBufferFlags);
+        f32x4 sq = zero4(), sk = zero4(), pq = zero4(), pk = zero4();
+        float xq[KH][4], xk[KH][4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
-        xq[m][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rqr, off, 0, 0));
-        xk[m][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rkr, off, 0, 0));
-        sq[r] += xq[m][r] * xq[m][r];
-        sk[r] += xk[m][r] * xk[m][r];
-        pq[r] += xq[m][r] * dQa[m][r];
-        pk[r] += xk[m][r] * dKa[m][r];
+        for (int m = 0; m < KH; ++m) {
+          const int ct = 2 * m + hf;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
+            xq[m][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rqr, off, 0, 0));
+            xk[m][r] = bf2f(__builtin_amdgcn_raw_buffer_load_b16(rkr, off, 0, 0));
+            sq[r] += xq[m][r] * xq[m][r];
+            sk[r] += xk[m][r] * xk[m][r];
+            pq[r] += xq[m][r] * dQa[m][r];
+            pk[r] += xk[m][r] * dKa[m][r];
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sq[r] = row16_sum(sq[r]);
+          sk[r] = row16_sum(sk[r]);
+          pq[r] = row16_sum(pq[r]);
+          pk[r] = row16_sum(pk[r]);
+        }
+        // combine the two column halves (RowP is free after the v-head loop)
+        if (r16 == 0) {
+          *reinterpret_cast<f32x4*>(&RowP[hf][0][row0]) = sq;
+          *reinterpret_cast<f32x4*>(&RowP[hf][1][row0]) = sk;
+          *reinterpret_cast<f32x4*>(&RowP[hf][2][row0]) = pq;
+          *reinterpret_cast<f32x4*>(&RowP[hf][3][row0]) = pk;
+        }
+        __syncthreads();
+        // dx = r (dy - y (y . dy)), y = x r, r = (|x|^2 + eps)^-1/2
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = row0 + r;
+          const float tq = RowP[0][0][i] + RowP[1][0][i], tk = RowP[0][1][i] + RowP[1][1][i];
+          const float uq = RowP[0][2][i] + RowP[1][2][i], uk = RowP[0][3][i] + RowP[1][3][i];
+          const float rq = rsqrtf(tq + 1e-6f), rk2 = rsqrtf(tk + 1e-6f);
+#pragma unroll
+          for (int m = 0; m < KH; ++m) {
+            dQa[m][r] = rq * (dQa[m][r] - xq[m][r] * rq * rq * uq);
+            dKa[m][r] = rk2 * (dKa[m][r] - xk[m][r] * rk2 * rk2 * uk);
+          }
+        }
       }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sq[r] = row16_sum(sq[r]);
-      sk[r] = row16_sum(sk[r]);
-      pq[r] = row16_sum(pq[r]);
-      pk[r] = row16_sum(pk[r]);
-    }
-    // combine the two column halves (RowP is free after the v-head loop)
-    if (r16 == 0) {
-      *reinterpret_cast<f32x4*>(&RowP[hf][0][row0]) = sq;
-      *reinterpret_cast<f32x4*>(&RowP[hf][1][row0]) = sk;
-      *reinterpret_cast<f32x4*>(&RowP[hf][2][row0]) = pq;
-      *reinterpret_cast<f32x4*>(&RowP[hf][3][row0]) = pk;
-    }
-    __syncthreads();
-    // dx = r (dy - y (y . dy)), y = x r, r = (|x|^2 + eps)^-1/2
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = row0 + r;
-      const float tq = RowP[0][0][i] + RowP[1][0][i], tk = RowP[0][1][i] + RowP[1][1][i];
-      const float uq = RowP[0][2][i] + RowP[1][2][i], uk = RowP[0][3][i] + RowP[1][3][i];
-      const float rq = rsqrtf(tq + 1e-6f), rk2 = rsqrtf(tk + 1e-6f);
 #pragma unroll
       for (int m = 0; m < KH; ++m) {
-        dQa[m][r] = rq * (dQa[m][r] - xq[m][r] * rq * rq * uq);
-        dKa[m][r] = rk2 * (dKa[m][r] - xk[m][r] * rk2 * rk2 * uk);
+        const int ct = 2 * m + hf;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
+          __builtin_amdgcn_raw_buffer_store_b16(f2bf(dQa[m][r]), rdq, off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(f2bf(dKa[m][r]), rdk, off, 0, 0);
+        }
       }
     }
-  }
-#pragma unroll
-  for (int m = 0; m < KH; ++m) {
-    const int ct = 2 * m + hf;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int off = ((row0 + r) * Hqk * K + 16 * ct + r16) * 2;
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dQa[m][r]), rdq, off, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dKa[m][r]), rdk, off, 0, 0);
-    }
+    if (!more) break;
+    // the next item's K / Q rows (Ks / Qs are free since the last v-head's
+    // closing barrier; requested earlier, into registers carried to the next
+    // item, they spill)
+    stage_kq(nxt);
+    cur = nxt;
+    x = xn;
   }
 }
 
@@ -800,10 +857,15 @@ static void launch_bwd_kernels(const uint16_t* q, const uint16_t* k, const uint1
   ws.dd = reinterpret_cast<uint16_t*>(wsb + p.dd);
   const int total = B * T;
   launch_rev_sw<K>(kn, dO, dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws.f, ws.dse, ws.dd, st);
-  if (p.ncmax > 0)
-    hipLaunchKernelGGL((chunk_grad_kernel<K, V>), dim3((unsigned)p.ncmax, Hqk), dim3(kGradThreads), 0,
-                       st, qn, kn, q, k, v, dO, beta, cu, N, T, total, Hqk, Hv, scale,
+  if (p.ncmax > 0) {
+    // one resident workgroup per CU (the kernel's LDS allows no second),
+    // each taking every grid-th (chunk, qk-head) item
+    const long long items = p.ncmax * (long long)Hqk;
+    const int grid = (int)std::min<long long>(items, device_cus());
+    hipLaunchKernelGGL((chunk_grad_kernel<K, V>), dim3(grid), dim3(kGradThreads), 0, st, qn, kn,
+                       q, k, v, dO, beta, cu, N, T, total, Hqk, Hv, (int)p.ncmax, scale,
                        l2 ? 1 : 0, ws, dq, dk, dv, dg, dbeta);
+  }
 }
 
 }  // namespace gdn
@@ -859,7 +921,8 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
     return gdn_host::fail(GDN_ERR_WORKSPACE, "gdn_chunk_bwd: workspace needs " +
                                                  std::to_string(p.total) + " bytes, got " +
                                                  std::to_string(workspace_bytes));
-  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31))
+  if (p.ncmax > (1LL << 30) || (long long)N * Hv * (V / 16) >= (1LL << 31) ||
+      p.ncmax * (long long)Hqk >= (1LL << 30))
     return gdn_host::fail(GDN_ERR_SHAPE, "gdn_chunk_bwd: problem too large");
   auto* wsb = static_cast<unsigned char*>(workspace);
   auto st = static_cast<hipStream_t>(stream);

@@ -561,20 +561,6 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
   }
 }
 
-// Compute units of the current device, looked up once per device.
-static int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    cache[dev] = cus;
-  }
-  return cache[dev];
-}
-
 template <int K, bool SAVE, bool OUT>
 void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
                      float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,

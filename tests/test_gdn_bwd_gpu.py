@@ -130,6 +130,12 @@ def test_bwd_l2norm(rocm_device):
     _case(rocm_device, 1, 150, 2, 4, 128, 128, seed=23, l2=True, what="l2norm")
 
 
+def test_bwd_l2norm_many_items(rocm_device):
+    """use_qk_l2norm with more (chunk, qk-head) items (150 x 4 = 600) than the gradient kernel
+    has resident workgroups, so that each workgroup goes through its item loop several times."""
+    _case(rocm_device, 1, 9600, 4, 8, 128, 128, seed=26, l2=True, what="l2norm 600 items")
+
+
 def test_bwd_no_dht_no_h0(rocm_device):
     _case(rocm_device, 1, 128, 2, 4, 128, 128, seed=24, h0_scale=0.0, dht_scale=0.0,
           what="no h0 / dht")
