@@ -209,17 +209,16 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   int qkbytes = 0, vbytes = 0;
 
   // K / Q rows of an item's chunk (rows >= L read as zero) into Ks / Qs,
-  // through registers that live only here
+  // through registers: requested by load_kq, written by store_kq
   constexpr int NQ = 64 * K / 8 / NTH;   // 16-byte chunks per thread
-  auto stage_kq = [&](const Item& it) {
+  auto load_kq = [&](const Item& it, bool live, u16x8 (&kr)[NQ], u16x8 (&qr)[NQ]) {
     int tid = threadIdx.x;   // (re-formed per call: see the v-head body)
     asm volatile("" : "+v"(tid));
-    const int nb = it.L * Hqk * K * 2;
+    const int nb = live ? it.L * Hqk * K * 2 : 0;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(k + ((size_t)it.t0 * Hqk + it.hq) * K), 0, nb, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(q + ((size_t)it.t0 * Hqk + it.hq) * K), 0, nb, kBufferFlags);
-    u16x8 kr[NQ], qr[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int idx = tid + NTH * i, r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
@@ -227,6 +226,10 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       kr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
       qr[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
     }
+  };
+  auto store_kq = [&](const u16x8 (&kr)[NQ], const u16x8 (&qr)[NQ]) {
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int idx = tid + NTH * i, r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
@@ -334,7 +337,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   // (of this item or the next).  It is made unconditionally: a conditional
   // one keeps the previous operands live through the whole v-head for the
   // path that skips it, which spills.
-  auto vhead = [&](int gi, auto prefetch) {
+  auto vhead = [&](int gi, auto prefetch, auto after_dk) {
     // The lane index is passed through an empty asm statement once per
     // v-head, so the many per-lane LDS / buffer addresses derived from it are
     // formed inside the loop where they are used, instead of being hoisted
@@ -683,6 +686,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
     }
 
+    after_dk();
+
     // ---- row partials: reduce over the 16 lanes of a group, then combine
     // the two column halves through LDS
 #pragma unroll
@@ -732,7 +737,11 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     __syncthreads();   // LDS reuse by the next v-head
   };
   issue_stage(cur, 0, true);
-  stage_kq(cur);
+  {
+    u16x8 kr[NQ], qr[NQ];
+    load_kq(cur, true, kr, qr);
+    store_kq(kr, qr);
+  }
   for (;;) {
     __syncthreads();
     ci = cur.ci;
@@ -750,8 +759,14 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     Item nxt;
     const bool more = find_item(xn, nxt);
     if (!more) nxt = cur;
-    for (int gi = 0; gi + 1 < Gn; ++gi) vhead(gi, [&] { issue_stage(cur, gi + 1, true); });
-    vhead(Gn - 1, [&] { issue_stage(nxt, 0, more); });
+    // the next item's K / Q rows are requested once the last v-head's dK / dQ
+    // products are issued (their registers then free) and written to Ks / Qs
+    // after this item's dq / dk stores (Ks / Qs free since the last v-head's
+    // closing barrier; the wait for them counts none of those stores)
+    u16x8 kr[NQ], qr[NQ];
+    for (int gi = 0; gi + 1 < Gn; ++gi)
+      vhead(gi, [&] { issue_stage(cur, gi + 1, true); }, [] {});
+    vhead(Gn - 1, [&] { issue_stage(nxt, 0, more); }, [&] { load_kq(nxt, more, kr, qr); });
 
     // ---- dq, dk: through the l2norm when the forward normalised q, k
     // (the lane indices re-formed here, as in the v-head body, so that the
@@ -829,10 +844,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
       }
     }
     if (!more) break;
-    // the next item's K / Q rows (Ks / Qs are free since the last v-head's
-    // closing barrier; requested earlier, into registers carried to the next
-    // item, they spill)
-    stage_kq(nxt);
+    store_kq(kr, qr);
     cur = nxt;
     x = xn;
   }
