@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   f32x4 dQa[KH], dKa[KH];   // column tiles 2m + hf
 
   // Operands of a v-head's staging phase (slices 0..2 of S / dS' or d / V,
-  // T, the dd rows, G and beta, the A fragments of dO / dd / d), requested
+  // T, the dd rows, G and beta, the A fragments of dO / d), requested
   // into registers: for the first item's first v-head before the loop, for
   // every later v-head (of this item or the next) before the previous
   // v-head's dK / dQ products, so their latency overlaps that v-head's last
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   u16x8 pre[3][2];
   f32x4 tv[NT];
   u16x8 dv8[ND];
-  u16x8 aO[VB], aD[VB], aL[VB];
+  u16x8 aO[VB], aL[VB];
   float gsv = 0.f, bsv = 0.f;
   auto issue_stage = [&](const Item& it, int gi_t, bool live) {
     int tid = threadIdx.x;
@@ -329,7 +329,6 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     for (int b = 0; b < VB; ++b) {
       const int off = (rowA * Hv * V + 32 * b + 8 * grp) * 2;
       aO[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
-      aD[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, off, 0, 0));
       aL[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
     }
   };
@@ -435,6 +434,10 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     }
     __syncthreads();
 
+    // A fragments of dd (this wave's rows) from the staged dd rows
+    u16x8 aD[VB];
+#pragma unroll
+    for (int b = 0; b < VB; ++b) aD[b] = *reinterpret_cast<const u16x8*>(&dds[rowA][32 * b + 8 * grp]);
     // row factors of this lane's OL rows
     const float GL = Gs[L - 1];
     f32x4 eg, dec, bt;
