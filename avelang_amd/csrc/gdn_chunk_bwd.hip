@@ -124,6 +124,12 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   constexpr int LK = K + 8, LV = V + 8, LT = 68, LC = 72;
   constexpr int NSS = K / 32;          // slices of S / dS' (32 state rows each)
   constexpr int NSL = NSS + 2;         // + two slices of d / V (32 token rows each)
+  // Slices stream in the order d / V token slices first, then the state
+  // slices: a wave takes the A fragments of d for its rows from the token
+  // slice that holds them, for the state slices' d dS'^T products.
+  // Position i of the stream -> slice index (state slices 0..NSS-1, token
+  // slice t = NSS + t).
+  auto slice_at = [](int i) { return i < 2 ? NSS + i : i - 2; };
   constexpr int NPOS = 32 * V / 8;     // 16-byte positions of one matrix in a slice
   static_assert(NPOS <= NTH, "one staged position per thread");
   __shared__ __attribute__((aligned(16))) uint16_t Ks[64][LK];
@@ -135,7 +141,13 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
                                                                         : 2 * 2 * 32 * LV * 2;
   __shared__ __attribute__((aligned(16))) unsigned char StgRaw[kStgBytes];
   uint16_t (*StgS)[2][V][LS] = reinterpret_cast<uint16_t (*)[2][V][LS]>(StgRaw);
-  uint16_t (*Stg)[2][32][LV] = reinterpret_cast<uint16_t (*)[2][32][LV]>(StgRaw);
+  // token buffer 1 sits at the top of the stage, clear of state buffer 0:
+  // state slice 0 is written while token slice 1 is read
+  constexpr int kTokBuf = 2 * 32 * LV * 2;
+  static_assert(2 * V * LS * 2 <= kStgBytes - kTokBuf, "token buffer 1 must clear state buffer 0");
+  uint16_t (*const Stg[2])[32][LV] = {
+      reinterpret_cast<uint16_t (*)[32][LV]>(StgRaw),
+      reinterpret_cast<uint16_t (*)[32][LV]>(StgRaw + kStgBytes - kTokBuf)};
   __shared__ __attribute__((aligned(16))) float T32[64][LT];
   __shared__ __attribute__((aligned(16))) float X32[64][LT];
   __shared__ __attribute__((aligned(16))) uint16_t Tb16[64][LC];
@@ -251,7 +263,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   f32x4 dQa[KH], dKa[KH];   // column tiles 2m + hf
 
   // Operands of a v-head's staging phase (slices 0..2 of S / dS' or d / V,
-  // T, the dd rows, G and beta, the A fragments of dO / d), requested
+  // T, the dd rows, G and beta, the A fragments of dO), requested
   // into registers: for the first item's first v-head before the loop, for
   // every later v-head (of this item or the next) before the previous
   // v-head's dK / dQ products, so their latency overlaps that v-head's last
@@ -264,7 +276,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
   u16x8 pre[3][2];
   f32x4 tv[NT];
   u16x8 dv8[ND];
-  u16x8 aO[VB], aL[VB];
+  u16x8 aO[VB];
   float gsv = 0.f, bsv = 0.f;
   auto issue_stage = [&](const Item& it, int gi_t, bool live) {
     int tid = threadIdx.x;
@@ -297,15 +309,16 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
     if (tid < NPOS) {
 #pragma unroll
-      for (int sl = 0; sl < 3 && sl < NSL; ++sl) {
+      for (int i = 0; i < 3 && i < NSL; ++i) {
+        const int sl = slice_at(i);
         if (sl < NSS) {
           const int so = 32 * sl * 2;
-          pre[sl][0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rS, sp_vs, so, 0));
-          pre[sl][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rE, sp_vs, so, 0));
+          pre[i][0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rS, sp_vs, so, 0));
+          pre[i][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rE, sp_vs, so, 0));
         } else {
           const int so = 32 * (sl - NSS) * Hv * V * 2;
-          pre[sl][0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_vt, so, 0));
-          pre[sl][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, sp_vt, so, 0));
+          pre[i][0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_vt, so, 0));
+          pre[i][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, sp_vt, so, 0));
         }
       }
     }
@@ -329,7 +342,6 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     for (int b = 0; b < VB; ++b) {
       const int off = (rowA * Hv * V + 32 * b + 8 * grp) * 2;
       aO[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
-      aL[b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0));
     }
   };
   // One v-head of the group; prefetch() requests the next v-head's operands
@@ -371,10 +383,13 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
 
     // slice sl: state columns 32 sl..32 sl + 31 of every row of S^T (matrix
     // 0) and dS'^T (matrix 1) for sl < NSS (both stored transposed, [V][K]),
-    // token rows 32 (sl - NSS).. of d (0) and V (1) after
+    // token rows 32 (sl - NSS).. of d (0) and V (1) after; load_slice and
+    // store_slice take the stream position i (slice slice_at(i), stage
+    // buffer i % 2)
     float sde = 0.f;   // partial <S, dS'> of the positions this thread stages
-    auto load_slice = [&](int sl, u16x8 (&buf)[2]) {
+    auto load_slice = [&](int i, u16x8 (&buf)[2]) {
       if (!stager) return;
+      const int sl = slice_at(i);
       if (sl < NSS) {
         const int so = 32 * sl * 2;
         buf[0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rS, sp_vs, so, 0));
@@ -385,14 +400,15 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         buf[1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, sp_vt, so, 0));
       }
     };
-    auto store_slice = [&](int sl, const u16x8 (&buf)[2]) {
+    auto store_slice = [&](int i, const u16x8 (&buf)[2]) {
       if (!stager) return;
+      const int sl = slice_at(i);
       if (sl < NSS) {
-        *reinterpret_cast<u16x8*>(&StgS[sl & 1][0][ss_v][ss_k]) = buf[0];
-        *reinterpret_cast<u16x8*>(&StgS[sl & 1][1][ss_v][ss_k]) = buf[1];
+        *reinterpret_cast<u16x8*>(&StgS[i & 1][0][ss_v][ss_k]) = buf[0];
+        *reinterpret_cast<u16x8*>(&StgS[i & 1][1][ss_v][ss_k]) = buf[1];
       } else {
-        *reinterpret_cast<u16x8*>(&Stg[sl & 1][0][sp_r][sp_c8]) = buf[0];
-        *reinterpret_cast<u16x8*>(&Stg[sl & 1][1][sp_r][sp_c8]) = buf[1];
+        *reinterpret_cast<u16x8*>(&Stg[i & 1][0][sp_r][sp_c8]) = buf[0];
+        *reinterpret_cast<u16x8*>(&Stg[i & 1][1][sp_r][sp_c8]) = buf[1];
       }
       if (sl < NSS) {
         // bf16 pairs straight into v_dot2_f32_bf16.  Each pair passes an
@@ -452,12 +468,19 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     // ---- streamed products over the slices (this wave: column tile hf of
     // each slice)
     f32x4 dpt[2], ddv[2];
+    u16x8 aL[VB];   // A fragments of d (this wave's rows), from its token slice
 #pragma unroll
-    for (int sl = 0; sl < NSL; ++sl) {
-      if (sl + 1 < NSL) store_slice(sl + 1, pre[(sl + 1) % 3]);
-      if (sl + 3 < NSL) load_slice(sl + 3, pre[(sl + 3) % 3]);
+    for (int i = 0; i < NSL; ++i) {
+      const int sl = slice_at(i);
+      if (i + 1 < NSL) store_slice(i + 1, pre[(i + 1) % 3]);
+      if (i + 3 < NSL) load_slice(i + 3, pre[(i + 3) % 3]);
       __builtin_amdgcn_sched_barrier(0);
-      const int bufi = sl & 1;
+      const int bufi = i & 1;
+      if (sl >= NSS && (rt >> 1) == sl - NSS) {
+#pragma unroll
+        for (int b = 0; b < VB; ++b)
+          aL[b] = *reinterpret_cast<const u16x8*>(&Stg[bufi][0][16 * (rt & 1) + r16][32 * b + 8 * grp]);
+      }
       f32x4 x0 = zero4(), x1 = zero4(), x2 = zero4();
 #pragma unroll
       for (int b = 0; b < VB; ++b) {
