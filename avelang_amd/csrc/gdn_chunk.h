@@ -4,6 +4,8 @@
 // reuses to recompute (and save) the forward chain.
 #pragma once
 
+#include <atomic>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -14,10 +16,16 @@ struct ChunkWs {
   int32_t* off;     // [N+1] first global chunk of each sequence
   int32_t* status;  // [1] 0, or the cu_seqlens violation the chunk table found
   float* gate;      // [NC][Hv][64]: G_i, the chunk-local cumulative log-decay
-  u16x8* tfrag;     // [NC][Hv][4 row tiles][2 k-blocks][2 hi/lo][64 lanes]
-  u16x8* pfrag;     // [NC][Hv][4][2][64] (not written by the backward's recomputation)
-  uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] (use_qk_l2norm only),
-  uint16_t* kn;     // written by the prep kernel, read by the chain
+  u16x8* tfrag;     // [NC][Hv][6 slots][64 lanes] fp16 A-operand fragments of Tb,
+                    // rows in the chain's rho order, slot tb_slot(row tile, k-block)
+  u16x8* pfrag;     // [NC][Hv][6][64] fp16 A-operand fragments of P, natural rows
+                    // (not written by the backward's recomputation)
+  unsigned char* k16;  // [NC][Hqk][KLayout<K>::BYTES] the chunk's K rows as fp16 in
+                       // the chain's LDS layout (rows past the sequence end 0)
+  u16x8* q16;       // [NC][Hqk][4 row tiles][K/32 k-blocks][64] fp16 B-operand
+                    // fragments of the chunk's Q rows (forms that write o)
+  uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] bf16 (use_qk_l2norm with
+  uint16_t* kn;     // the backward), written by the prep kernel
   // backward only
   float* tmat;      // [NC][Hv][10][16][16] T = (I + A)^-1 (fp32): its lower 16 x 16
                     // blocks (rt, cb), cb <= rt, in the order tmat_block() gives,
@@ -41,19 +49,24 @@ __host__ __device__ constexpr int tmat_block_row(int bi) {
   return bi >= 6 ? 3 : (bi >= 3 ? 2 : (bi >= 1 ? 1 : 0));
 }
 
-// Compute units of the current device, looked up once per device.
+// Devices the library keeps per-device state for (compute-unit counts here,
+// the no-allocation scratch address in gdn_chunk.hip).
+constexpr int kMaxDevices = 256;
+
+// Compute units of the current device, looked up once per device (any host
+// thread may call this; the cache entries are atomic).
 inline int device_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int cus = cache[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    cache[dev] = cus;
+    cache[dev].store(cus, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return cus;
 }
 
 __device__ __forceinline__ void seq_bounds(const int32_t* cu, int n, int T, int total,
@@ -127,8 +140,8 @@ __device__ __forceinline__ u16x8 cat8(u16x4 a, u16x4 b) {
   return u16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Tb fragment slot of (row tile ti, k-block b): row tiles 0 and 1 have no
-// k-block 1 (Tb is lower triangular), so six slots per hi / lo part.
+// Tb / P fragment slot of (row tile ti, k-block b): row tiles 0 and 1 have
+// no k-block 1 (both are lower triangular), so six slots.
 __device__ __forceinline__ constexpr int tb_slot(int ti, int b) { return b == 0 ? ti : 2 + ti; }
 
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n
@@ -154,7 +167,7 @@ struct KLayout {
 
 // Workspace plan (byte offsets into the caller's buffer).
 struct WsPlan {
-  size_t off, status, gate, tfrag, pfrag, qn, kn, total;
+  size_t off, status, gate, tfrag, pfrag, k16, q16, qn, kn, total;
   // backward only (0 when not planned)
   size_t tmat, ttfrag, ptfrag, qtfrag, hs, dl, dse, dd;
   long long ncmax;
@@ -180,9 +193,9 @@ ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb);
 // Forward chain, state-wave form (gdn_chunk_chain.hip).  SAVE: the state at
 // every chunk start and the per-token deltas for the backward; OUT: o, ht.
 template <int K, bool SAVE, bool OUT>
-void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
-                     float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
-                     int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st);
+void launch_chain_sw(const uint16_t* v, const float* h0, float* ht, uint16_t* o,
+                     const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
+                     float scale, const ChunkWs& ws, hipStream_t st);
 
 // Reverse chain of the backward (gdn_chunk_rev.hip): dS' of every chunk into
 // dse, dd into dd, dh0.

@@ -255,15 +255,35 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 #pragma unroll
     for (int b = 0; b < KB; ++b)
       *reinterpret_cast<u16x8*>(&Ks[16 * w + r16][32 * b + 8 * grp]) = ka[b];
-    // the normalised rows for the chain, stored after the LDS writes above
-    // (stores count in the same in-order vector-memory counter as the loads,
-    // so a wait for ka ahead of them would also wait for these stores)
-    if (L2 && h % (Hv / Hqk) == 0 && 16 * w + r16 < L) {
-      const size_t wo = ((size_t)(t0 + 16 * w + r16) * Hqk + hq) * K + 8 * grp;
+    // The first v-head of each qk-head group stores the chunk's K rows and Q
+    // fragments as fp16 for the chain (after the LDS writes above: stores
+    // count in the same in-order vector-memory counter as the loads, so a
+    // wait for ka ahead of them would also wait for these stores).  K goes
+    // in the chain's LDS layout with rows past the sequence end zeroed, so
+    // the chain copies it to LDS with contiguous loads; Q as the B-operand
+    // fragments the chain's output wave loads (row 16 w + r16, columns
+    // 32 b + 8 grp ..).
+    if (h % (Hv / Hqk) == 0) {
+      using KL = KLayout<K>;
+      const int row = 16 * w + r16;
+      unsigned char* kd = ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES + KL::row(row);
 #pragma unroll
-      for (int b = 0; b < KB; ++b) {
-        *reinterpret_cast<u16x8*>(ws.kn + wo + 32 * b) = ka[b];
-        *reinterpret_cast<u16x8*>(ws.qn + wo + 32 * b) = qa[b];
+      for (int b = 0; b < KB; ++b)
+        *reinterpret_cast<u16x8*>(kd + 16 * (4 * b + grp)) =
+            row < L ? bf2h8(ka[b]) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if constexpr (OUT) {
+        u16x8* qd = ws.q16 + (((size_t)ci * Hqk + hq) * 4 + w) * KB * 64 + lane;
+#pragma unroll
+        for (int b = 0; b < KB; ++b) qd[b * 64] = bf2h8(qa[b]);
+      }
+      // the normalised rows (bf16) for the backward's kernels
+      if (L2 && BWD && row < L) {
+        const size_t wo = ((size_t)(t0 + row) * Hqk + hq) * K + 8 * grp;
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+          *reinterpret_cast<u16x8*>(ws.kn + wo + 32 * b) = ka[b];
+          *reinterpret_cast<u16x8*>(ws.qn + wo + 32 * b) = qa[b];
+        }
       }
     }
   }
@@ -302,7 +322,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     }
     *reinterpret_cast<f32x4*>(&AdT[w][r16][4 * grp]) = av;
   }
-  const size_t pbase = (((size_t)ci * Hv + h) * 4 + w) * 2;
+  u16x8* pdst = ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64;
   typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int tc = 0; tc < 4; ++tc) {
@@ -316,24 +336,23 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       }
     }
     const f32x4 Gj = *reinterpret_cast<const f32x4*>(&Gs[16 * tc + 4 * grp]);
-    f32x4 av;
-    u16x4 pv;
+    f32x4 av, pf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = 16 * tc + 4 * grp + r;
       const float gam = (tc <= w && j <= i) ? __expf(Gi - Gj[r]) : 0.f;
       av[r] = (j < i) ? Bi * kt[r] * gam : 0.f;
-      pv[r] = f2bf(scale * pt[r] * gam);
+      pf[r] = scale * pt[r] * gam;
     }
     if (tc < w) *reinterpret_cast<f32x4*>(&Ab[w * (w - 1) / 2 + tc][r16][4 * grp]) = av;
-    if constexpr (BWD) *reinterpret_cast<u16x4*>(&Ps[i][16 * tc + 4 * grp]) = pv;
-    // P fragment slot: k-block tc/2, fragment lane r16 + 16 (2 (tc%2) + grp/2),
-    // elements 4 (grp%2) .. +3
+    if constexpr (BWD) *reinterpret_cast<u16x4*>(&Ps[i][16 * tc + 4 * grp]) = f2bf4(pf);
+    // P fragment (fp16): slot tb_slot(w, tc / 2), fragment lane
+    // r16 + 16 (2 (tc % 2) + grp / 2), elements 4 (grp % 2) .. + 3
     // (k-block 1 of row tiles 0 and 1 is zero and never read: not stored)
     if (OUT && (tc < 2 || w >= 2)) {
-      const size_t pf = (pbase + tc / 2) * 64 + r16 + 16 * (2 * (tc % 2) + grp / 2);
-      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(ws.pfrag + pf) + 4 * (grp % 2)) =
-          __builtin_bit_cast(u32x2, pv);
+      uint16_t* pe = reinterpret_cast<uint16_t*>(
+          pdst + tb_slot(w, tc / 2) * 64 + r16 + 16 * (2 * (tc % 2) + grp / 2));
+      *reinterpret_cast<u32x2*>(pe + 4 * (grp % 2)) = __builtin_bit_cast(u32x2, f2h4(pf));
     }
   }
   __syncthreads();
@@ -409,30 +428,32 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     __syncthreads();
   }
 
-  // A-operand fragments: row 16w + r16, k = 32b + 8grp + ii
+  // Tb = T diag(beta) as fp16 A-operand fragments in the chain's row order:
+  // natural row R = 16 w + r16 is row m = 4 ((R / 8) % 4) + R % 4 of rho
+  // tile ti = 2 (R / 32) + (R / 4) % 2; lane m + 16 grp of slot tb_slot(ti, b)
+  // holds k = 32 b + 8 grp .. + 7
   const size_t base = ((size_t)ci * Hv + h) * 4 + w;
   const int row = 16 * w + r16;
+  {
+    const int ti = 2 * (w >> 1) + ((r16 >> 2) & 1);
+    const int m = 4 * (2 * (w & 1) + (r16 >> 3)) + (r16 & 3);
+    u16x8* tdst = ws.tfrag + ((size_t)ci * Hv + h) * 6 * 64 + m + 16 * grp;
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    if (b == 1 && w < 2) break;   // zero block, never read by the chain
-    const int c0 = 32 * b + 8 * grp;
-    const f32x4 t0v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0]);
-    const f32x4 t1v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0 + 4]);
-    const f32x4 b0v = *reinterpret_cast<const f32x4*>(&Bs[c0]);
-    const f32x4 b1v = *reinterpret_cast<const f32x4*>(&Bs[c0 + 4]);
-    u16x8 th, tl;
+    for (int b = 0; b < 2; ++b) {
+      if (b == 1 && w < 2) break;   // zero block, never read by the chain
+      const int c0 = 32 * b + 8 * grp;
+      const f32x4 t0v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0]);
+      const f32x4 t1v = *reinterpret_cast<const f32x4*>(&Tm[row * kLdA + c0 + 4]);
+      const f32x4 b0v = *reinterpret_cast<const f32x4*>(&Bs[c0]);
+      const f32x4 b1v = *reinterpret_cast<const f32x4*>(&Bs[c0 + 4]);
+      f32x4 x0, x1;
 #pragma unroll
-    for (int ii = 0; ii < 8; ++ii) {
-      const float tv = ii < 4 ? t0v[ii] : t1v[ii - 4];
-      const float bb = ii < 4 ? b0v[ii] : b1v[ii - 4];
-      const float x = (c0 + ii <= row) ? tv * bb : 0.f;
-      uint16_t xh, xl;
-      split_bf(x, xh, xl);
-      th[ii] = xh;
-      tl[ii] = xl;
+      for (int ii = 0; ii < 4; ++ii) {
+        x0[ii] = (c0 + ii <= row) ? t0v[ii] * b0v[ii] : 0.f;
+        x1[ii] = (c0 + 4 + ii <= row) ? t1v[ii] * b1v[ii] : 0.f;
+      }
+      tdst[tb_slot(ti, b) * 64] = cat8(f2h4(x0), f2h4(x1));
     }
-    ws.tfrag[((base * 2 + b) * 2 + 0) * 64 + lane] = th;
-    ws.tfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
   }
   if constexpr (BWD) {
     // Tb^T fragments, row tile w: Tb^T[m][kk] = T[kk][m] beta_m (kk >= m);
@@ -487,10 +508,13 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
   p.off = take((size_t)(N + 1) * 4);
   p.status = take(4);
   p.gate = take(nch * 64 * 4);
-  p.tfrag = take(nch * 4 * 2 * 2 * 64 * 16);
-  p.pfrag = take(nch * 4 * 2 * 64 * 16);
+  p.tfrag = take(nch * 6 * 64 * 16);
+  p.pfrag = take(nch * 6 * 64 * 16);
+  const size_t nqk = (size_t)p.ncmax * Hqk;   // (chunk, qk-head) pairs
+  p.k16 = take(nqk * (K == 128 ? KLayout<128>::BYTES : KLayout<64>::BYTES));
+  p.q16 = take(nqk * 64 * K * 2);
   p.qn = p.kn = at;
-  if (l2) {
+  if (l2 && bwd) {
     p.qn = take((size_t)total * Hqk * K * 2);
     p.kn = take((size_t)total * Hqk * K * 2);
   }
@@ -515,6 +539,8 @@ ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb) {
   ws.gate = reinterpret_cast<float*>(wsb + p.gate);
   ws.tfrag = reinterpret_cast<u16x8*>(wsb + p.tfrag);
   ws.pfrag = reinterpret_cast<u16x8*>(wsb + p.pfrag);
+  ws.k16 = wsb + p.k16;
+  ws.q16 = reinterpret_cast<u16x8*>(wsb + p.q16);
   ws.qn = reinterpret_cast<uint16_t*>(wsb + p.qn);
   ws.kn = reinterpret_cast<uint16_t*>(wsb + p.kn);
   if (p.hs) {
@@ -547,9 +573,10 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
       hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, OUT, false>), dim3((unsigned)p.ncmax, Hv), dim3(256),
                          0, st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws, gate);
   }
-  // with use_qk_l2norm the chain reads the rows the prep kernel normalised
-  launch_chain_sw<K, BWD, OUT>(l2 ? ws.qn : q, l2 ? ws.kn : k, v, h0, OUT ? ht : nullptr,
-                               OUT ? o : nullptr, cu, N, T, total, Hqk, Hv, V, scale, ws, st);
+  // the chain reads K and Q as the prep kernel's fp16 copies (normalised
+  // with use_qk_l2norm)
+  launch_chain_sw<K, BWD, OUT>(v, h0, OUT ? ht : nullptr, OUT ? o : nullptr, cu, N, T, total,
+                               Hqk, Hv, V, scale, ws, st);
   // a cu_seqlens violation left every sequence empty: o is zero-filled (and
   // ht = h0, written by the chain for an empty sequence)
   if (cu && OUT) {
@@ -670,7 +697,7 @@ constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
-constexpr int kMaxDevices = 256;
+using gdn::kMaxDevices;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];   // address of `scratch` on each device, once looked up
 

@@ -48,22 +48,19 @@ namespace gdn {
 // GPU twice over).
 template <int K, bool SAVE, bool OUT, int NS>
 __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_chain_sw_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
     const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
     float scale, ChunkWs ws) {
   constexpr int KB = K / 32;   // k-blocks over the key index
   constexpr int ST = K / 16;   // 16-row state tiles
   // Stage buffers (chunk c in buffer c % 3): the chunk's K rows (KLayout),
-  // the Tb A fragments in rho row order, the V tile as fp32 in the state
-  // wave's layout (lane (n16, grp) of token tile ti reads
-  // Vst[.][ti][grp][4 n16 ..]; the padded rows put the stage wave's
-  // scattered writes on distinct banks), e^G and e^(G_last - G) by token,
-  // and e^G_last.
+  // the Tb A fragments in rho row order, the V tile as it sits in v (bf16,
+  // [token][16 columns] per slice), e^G and e^(G_last - G) by token, and
+  // e^G_last.
   using KL = KLayout<K>;
   __shared__ __attribute__((aligned(16))) unsigned char Kst[3][KL::BYTES];
-  __shared__ __attribute__((aligned(16))) u16x8 Tst[3][6][2][64];
-  __shared__ __attribute__((aligned(16))) float Vst[3][NS][4][4][68];
+  __shared__ __attribute__((aligned(16))) u16x8 Tst[3][6][64];
+  __shared__ __attribute__((aligned(16))) uint16_t Vrw[3][NS][64][16];
   __shared__ __attribute__((aligned(16))) float Gst[3][2][64];
   __shared__ float Egl[3];
   // Output buffers (chunk c in buffer c % 3), left by the state wave for
@@ -137,7 +134,7 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       constexpr int b3 = decltype(b3c)::value;
       const unsigned char* Kb = Kst[b3];
       // operands of the step, all from LDS and issued first
-      u16x8 ka[KB][4], ta[6][2];
+      u16x8 ka[KB][4], ta[6];
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
 #pragma unroll
@@ -145,58 +142,43 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
           ka[b][ti] = *reinterpret_cast<const u16x8*>(Kb + ka_off[ti] + 64 * b);
       }
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        ta[i][0] = Tst[b3][i][0][lane];
-        ta[i][1] = Tst[b3][i][1][lane];
-      }
+      for (int i = 0; i < 6; ++i) ta[i] = Tst[b3][i][lane];
       f32x4 eg[4], dc[4], vv[4];
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
         const int r0 = 32 * (ti >> 1) + 8 * grp + 4 * (ti & 1);
         eg[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][0][r0]);
         dc[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][1][r0]);
-        vv[ti] = *reinterpret_cast<const f32x4*>(&Vst[b3][vs][ti][grp][4 * r16]);
+        // V at tokens rho(16 ti + 4 grp + r) = r0 + r, column r16: one
+        // transposing read of the 4 token rows
+        const u16x4 v4 = lds_tr16(&Vrw[b3][vs][r0 + (r16 >> 2)][4 * (r16 & 3)]);
+        vv[ti] = f32x4{bf2f(v4[0]), bf2f(v4[1]), bf2f(v4[2]), bf2f(v4[3])};
       }
       const float egl = Egl[b3];
 
       // X = K S on the four rho-ordered token tiles, k-block by k-block:
-      // the split of state tiles 2b, 2b+1 feeds k-block b
+      // state tiles 2b, 2b+1 (rounded to fp16) feed k-block b
       f32x4 X[4];
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) X[ti] = zero4();
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
-        u16x4 h0v, l0v, h1v, l1v;
-        split_bf4(S[2 * b], h0v, l0v);
-        split_bf4(S[2 * b + 1], h1v, l1v);
-        const u16x8 sh = cat8(h0v, h1v), sl = cat8(l0v, l1v);
+        const u16x8 sh = cat8(f2h4(S[2 * b]), f2h4(S[2 * b + 1]));
         Sx[b3][vs][b][lane] = sh;   // for this chunk's Q S (output wave)
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sh, X[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sl, X[ti]);
+        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16h(ka[b][ti], sh, X[ti]);
       }
-      // Y = V - e^G X (B fragments, hi and lo) and vnew = Tb Y, k-block 0
-      // first: row tiles 0 and 1 of vnew are then complete
-      auto ysplit = [&](int b, u16x8& yh, u16x8& yl) {
-        u16x4 hh0, ll0, hh1, ll1;
-        split_bf4(vv[2 * b] - eg[2 * b] * X[2 * b], hh0, ll0);
-        split_bf4(vv[2 * b + 1] - eg[2 * b + 1] * X[2 * b + 1], hh1, ll1);
-        yh = cat8(hh0, hh1);
-        yl = cat8(ll0, ll1);
+      // Y = V - e^G X (B fragments) and vnew = Tb Y, k-block 0 first: row
+      // tiles 0 and 1 of vnew are then complete
+      auto yfrag = [&](int b) {
+        return cat8(f2h4(vv[2 * b] - eg[2 * b] * X[2 * b]),
+                    f2h4(vv[2 * b + 1] - eg[2 * b + 1] * X[2 * b + 1]));
       };
       f32x4 vn[4];
-#pragma unroll
-      for (int ti = 0; ti < 4; ++ti) vn[ti] = zero4();
       {
-        u16x8 yh, yl;
-        ysplit(0, yh, yl);
+        const u16x8 y0 = yfrag(0);
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 0)][0], yh, vn[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 0)][0], yl, vn[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 0)][1], yh, vn[ti]);
+        for (int ti = 0; ti < 4; ++ti) vn[ti] = mfma16h(ta[tb_slot(ti, 0)], y0, zero4());
       }
       // K^T fragments of the update: element i of lane (m, grp) for state
       // tile t, k-block b is K[32 b + 8 grp + i][rho(16 t + m)], two
@@ -213,30 +195,20 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
         }
       }
       {
-        u16x8 yh, yl;
-        ysplit(1, yh, yl);
+        const u16x8 y1 = yfrag(1);
 #pragma unroll
-        for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 1)][0], yh, vn[ti]);
-#pragma unroll
-        for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 1)][0], yl, vn[ti]);
-#pragma unroll
-        for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16(ta[tb_slot(ti, 1)][1], yh, vn[ti]);
+        for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16h(ta[tb_slot(ti, 1)], y1, vn[ti]);
       }
-      // U = e^(G_last - G) vnew (hi, lo) and vnew (bf16) for the output;
-      // S = e^G_last S + K^T U, k-block by k-block
+      // U = e^(G_last - G) vnew and vnew itself (both fp16, the latter for
+      // the output wave); S = e^G_last S + K^T U, k-block by k-block
 #pragma unroll
       for (int t = 0; t < ST; ++t) S[t] = S[t] * egl;
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        u16x4 hh0, ll0, hh1, ll1;
-        split_bf4(dc[2 * b] * vn[2 * b], hh0, ll0);
-        split_bf4(dc[2 * b + 1] * vn[2 * b + 1], hh1, ll1);
-        const u16x8 uh = cat8(hh0, hh1), ul = cat8(ll0, ll1);
-        Vx[b3][vs][b][lane] = cat8(f2bf4(vn[2 * b]), f2bf4(vn[2 * b + 1]));
+        const u16x8 uh = cat8(f2h4(dc[2 * b] * vn[2 * b]), f2h4(dc[2 * b + 1] * vn[2 * b + 1]));
+        Vx[b3][vs][b][lane] = cat8(f2h4(vn[2 * b]), f2h4(vn[2 * b + 1]));
 #pragma unroll
-        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], uh, S[t]);
-#pragma unroll
-        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], ul, S[t]);
+        for (int t = 0; t < ST; ++t) S[t] = mfma16h(kt[b][t], uh, S[t]);
       }
       __syncthreads();   // chunk c's outputs published; stage buffer c % 3 free
     };
@@ -273,44 +245,39 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     // fence would wait for the loads still in flight for the next step),
     // with signal fences so that no LDS access moves across them.
     typedef __attribute__((address_space(3))) void* lds_ptr;
-    constexpr int P = K / 8;             // 16-byte pieces per K row
-    constexpr int kKT = KL::LOADS + 12;  // loads per stage: K blocks + Tb fragments
-    const int rowq = Hqk * K * 2;   // byte stride of a K row
+    constexpr int kKT = KL::LOADS + 6 + 2 * NS;  // loads per stage: K, Tb, V tiles
     // chunk j's data into buffer jb % 3 (past the last chunk the loads repeat
-    // it into a buffer no step reads, which keeps every step's count equal)
+    // it into a buffer no step reads, which keeps every step's count equal):
+    // the prep kernel's fp16 K block (already in KLayout, rows past the
+    // sequence end zero) and Tb fragments (already in rho row order), both
+    // contiguous, so lane l of load i copies bytes 16 (64 i + l)
     auto issue_kt = [&](int j, int jb) {
       const int ci = c_begin + j, buf = jb % 3;
-      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-      // K rows in KLayout: 16-byte unit p = 64 i + lane of the buffer is a
-      // piece of a row or padding (padding reads out of range, as 0); rows
-      // >= L read as 0
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(k + ((size_t)t0 * Hqk + hq) * K), 0, L * rowq, kBufferFlags);
+          ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES, 0, KL::BYTES, kBufferFlags);
 #pragma unroll
-      for (int i = 0; i < KL::LOADS; ++i) {
-        const int p = 64 * i + lane;
-        const int g16 = p / KL::GU, rem = p % KL::GU;
-        const int row = 16 * g16 + rem / (KL::RS / 16), piece = rem % (KL::RS / 16);
-        const bool data = rem < 16 * (KL::RS / 16) && piece < P && p < KL::UNITS;
+      for (int i = 0; i < KL::LOADS; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(Kst[buf] + 1024 * i), 16,
-                                                 data ? row * rowq + 16 * piece : 0x7ffffff0,
-                                                 0, 0, 0);
-      }
-      // Tb fragments gathered by rho row from the prep's natural fragments
+                                                 1024 * i + 16 * lane, 0, 0, 0);
       const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
-          ws.tfrag + ((size_t)ci * Hv + h) * 4 * 256, 0, 4 * 256 * 16, kBufferFlags);
+          ws.tfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-        const int row = rho_row(ti, r16);
-        const int src = (row >> 4) * 256 + (row & 15) + 16 * grp;
+      for (int i = 0; i < 6; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr)&Tst[buf][i][0], 16,
+                                                 1024 * i + 16 * lane, 0, 0, 0);
+      // V tiles: load x of slice sl, lane l copies half l % 2 of token row
+      // 32 x + l / 2 (rows past the sequence end read as 0)
+      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(v + (size_t)t0 * Hv * V), 0, L * Hv * V * 2, kBufferFlags);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          if (b == 1 && ti < 2) continue;
+      for (int sl = 0; sl < NS; ++sl) {
 #pragma unroll
-          for (int hl = 0; hl < 2; ++hl)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr)&Tst[buf][tb_slot(ti, b)][hl][0],
-                                                     16, (src + 128 * b + 64 * hl) * 16, 0, 0, 0);
-        }
+        for (int x = 0; x < 2; ++x)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rv, (lds_ptr)&Vrw[buf][sl][32 * x][0], 16,
+              ((32 * x + (lane >> 1)) * Hv * V + h * V + 16 * (vt0 + sl)) * 2 + 16 * (lane & 1),
+              0, 0, 0);
       }
     };
     auto barrier = [] {
@@ -339,63 +306,46 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     // every step issues the same loads and stores, so each wait names an
     // exact count.
     constexpr int kQP = OUT ? 4 * KB + 6 : 0;   // Q / P loads per chunk
-    constexpr int kVG = 2 * NS + 1;             // V tiles (2 per slice) + G (1)
+    constexpr int kVG = 1;                      // G
     // with both outputs, the saves go to a wave of their own (the last)
     constexpr bool kSplit = SAVE && OUT;
     constexpr int kSave = SAVE && !kSplit ? NS * (KB + 2) : 0;   // state and delta stores per chunk
     constexpr int kStep = (OUT ? 4 * NS : 0) + kSave + kQP + kVG;   // stores + loads per step
-    // Without o the V / G loads go before the saves, and the step's wait
-    // lets the previous step's saves stay in flight as well (the counter
-    // retires loads and stores in issue order): the stores then have two
-    // steps to drain instead of one, measured 2.5 % off the backward
-    constexpr int kWait = OUT ? kStep : kStep + kSave;
-    const int rowq = Hqk * K * 2;
+    // The stores of a step (o tiles, or the saves) go after its loads, and
+    // the step's wait lets the previous step's stores stay in flight as well
+    // (the counter retires loads and stores in issue order): the stores then
+    // have two steps to drain instead of one
+    constexpr int kStores = (OUT ? 4 * NS : 0) + kSave;
+    constexpr int kWait = kStep + kStores;
     struct Regs {
       u16x8 qf[4][KB];   // Q rows 16 ti + r16, B operand of (Q S)^T
       u16x8 pf[6];       // P fragments by tb_slot
-      u16x8 vr[NS][2];   // V tile row `lane`, 16 columns per slice
       float G;           // G of token `lane`
     };
     Regs rA, rB;
+    // the chunk's Q fragments (the prep kernel's fp16 copy) and P fragments,
+    // both contiguous 1 KiB blocks
     auto load_qp = [&](Regs& r, int j) {
       if constexpr (!OUT) return;
       const int ci = c_begin + j;
-      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
       const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(q + ((size_t)t0 * Hqk + hq) * K), 0, L * rowq, kBufferFlags);
+          ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
         for (int b = 0; b < KB; ++b)
           r.qf[ti][b] = __builtin_bit_cast(
-              u16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                         rq, (16 * ti + r16) * rowq + (32 * b + 8 * grp) * 2, 0, 0));
+              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16, 0, 0));
       }
       const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-          ws.pfrag + ((size_t)ci * Hv + h) * 4 * 128, 0, 4 * 128 * 16, kBufferFlags);
+          ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          if (b == 1 && ti < 2) continue;
-          r.pf[tb_slot(ti, b)] = __builtin_bit_cast(
-              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (ti * 128 + b * 64 + lane) * 16, 0, 0));
-        }
-      }
+      for (int i = 0; i < 6; ++i)
+        r.pf[i] = __builtin_bit_cast(
+            u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (i * 64 + lane) * 16, 0, 0));
     };
     auto load_vg = [&](Regs& r, int j) {
       const int ci = c_begin + j;
-      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V + 16 * vt0), 0,
-          (L - 1) * Hv * V * 2 + 32 * NS, kBufferFlags);
-#pragma unroll
-      for (int sl = 0; sl < NS; ++sl) {
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-          r.vr[sl][x] = __builtin_bit_cast(
-              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, lane * Hv * V * 2 + 32 * sl + 16 * x, 0, 0));
-      }
       const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<float*>(ws.gate + ((size_t)ci * Hv + h) * 64), 0, 256, kBufferFlags);
       r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
@@ -403,18 +353,6 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     auto write_vg = [&](const Regs& r, int j) {
       const int buf = j % 3;
       const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-      // token row t = lane sits at tile ti = 2 (t / 32) + (t / 4) % 2,
-      // lane (n16, (t / 8) % 4), element t % 4 of the state wave's layout
-      const int ti = 2 * (lane >> 5) + ((lane >> 2) & 1);
-#pragma unroll
-      for (int sl = 0; sl < NS; ++sl) {
-        float* dst = &Vst[buf][sl][ti][(lane >> 3) & 3][lane & 3];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          dst[4 * c] = bf2f(r.vr[sl][0][c]);
-          dst[4 * (c + 8)] = bf2f(r.vr[sl][1][c]);
-        }
-      }
       const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
       const float eg = __expf(r.G);
       Gst[buf][0][lane] = eg;
@@ -440,7 +378,7 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       if (live) {
 #pragma unroll
         for (int i = 0; i < KB; ++i)
-          sh[i] = Sx[b3][sl][c8 >> 2][(rpi * i + lane / cpr) + 16 * (c8 & 3)];
+          sh[i] = h2bf8(Sx[b3][sl][c8 >> 2][(rpi * i + lane / cpr) + 16 * (c8 & 3)]);
       }
       const size_t ci = live ? (size_t)(c_begin + j) : 0;
       const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
@@ -465,6 +403,8 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
           d0[c] = src[8 * c];
           d1[c] = src[8 * (c + 8)];
         }
+        d0 = h2bf8(d0);
+        d1 = h2bf8(d1);
       }
       const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr, drow, 0, 0);
@@ -473,16 +413,17 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     };
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     // o^T tiles of chunk j: lane (r16, grp) holds token row 16 ti + r16,
-    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile), and the
-    // chunk's saves when no save wave runs.  With live = false (no chunk
-    // yet) every store goes to an empty resource and is dropped.
-    auto output = [&](const Regs& r, int j, bool live) {
-      const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
+    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile).  Formed
+    // from register set r before the step's loads overwrite it, stored after
+    // them (stores retire in issue order with the loads, so a store issued
+    // ahead of the step's loads would hold up the next step's wait).  With
+    // live = false (no chunk yet) every store goes to an empty resource and
+    // is dropped.
+    struct OutTile {
+      u16x4 v[NS][4];
+    };
+    auto out_form = [&](const Regs& r, int j, bool live, OutTile& ot) {
       const int b3 = j % 3;
-      if constexpr (SAVE && !kSplit) save_chunk(j, live);
-      if constexpr (!OUT) return;
-      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-          o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
 #pragma unroll
       for (int sl = 0; sl < NS; ++sl) {
         u16x8 sh[KB], vx[2];
@@ -499,18 +440,29 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
             f32x4 qa = zero4(), qb = zero4();
 #pragma unroll
             for (int b = 0; b < KB; b += 2) {
-              qa = mfma16(sh[b], r.qf[ti][b], qa);
-              qb = mfma16(sh[b + 1], r.qf[ti][b + 1], qb);
+              qa = mfma16h(sh[b], r.qf[ti][b], qa);
+              qb = mfma16h(sh[b + 1], r.qf[ti][b + 1], qb);
             }
-            f32x4 pv = mfma16(vx[0], r.pf[tb_slot(ti, 0)], zero4());
-            if (ti >= 2) pv = mfma16(vx[1], r.pf[tb_slot(ti, 1)], pv);
+            f32x4 pv = mfma16h(vx[0], r.pf[tb_slot(ti, 0)], zero4());
+            if (ti >= 2) pv = mfma16h(vx[1], r.pf[tb_slot(ti, 1)], pv);
             const float egi = Gst[b3][0][16 * ti + r16];
             ov = f2bf4((scale * egi) * (qa + qb) + pv);
           }
-          __builtin_amdgcn_raw_buffer_store_b64(
-              __builtin_bit_cast(u32x2, ov), orsrc,
-              (((16 * ti + r16) * Hv + h) * V + 16 * (vt0 + sl) + 4 * grp) * 2, 0, 0);
+          ot.v[sl][ti] = ov;
         }
+      }
+    };
+    auto out_store = [&](const OutTile& ot, int j, bool live) {
+      const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+          __builtin_amdgcn_raw_buffer_store_b64(
+              __builtin_bit_cast(u32x2, ot.v[sl][ti]), orsrc,
+              (((16 * ti + r16) * Hv + h) * V + 16 * (vt0 + sl) + 4 * grp) * 2, 0, 0);
       }
     };
     if (kSplit && w == NS + 2) {
@@ -523,15 +475,24 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       if (nc > 0) save_chunk(nc - 1, true);
       return;
     }
+    // Every step issues its loads, then its stores (the o tiles, or without
+    // o the saves); the next step's wait leaves the previous step's stores
+    // and the current step's operations in flight, so each store has two
+    // steps to drain.  The prologue issues one such group per step before
+    // step 0 (loads for steps 0 and 1, stores dropped), so every wait of the
+    // loop names an exact count.
+    OutTile ot;
     if (nc > 0) {
       load_vg(rA, 0);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       write_vg(rA, 0);
       load_vg(rB, min(1, nc - 1));
-      output(rA, 0, false);             // the stores a step issues, dropped
+      if constexpr (OUT) out_store(ot, 0, false);
+      else save_chunk(0, false);
       load_qp(rA, 0);
       load_vg(rA, min(2, nc - 1));
-      if constexpr (!OUT) output(rA, 0, false);   // the previous step's saves
+      if constexpr (OUT) out_store(ot, 0, false);
+      else save_chunk(0, false);
     }
     __syncthreads();
     // step j works on register set (j + 1) % 2
@@ -539,12 +500,13 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWait));   // chunk j-1's Q / P, chunk j+1's V / G
       if (j + 1 < nc) write_vg(r, j + 1);
       if constexpr (OUT) {
-        output(r, j - 1, j >= 1);
+        out_form(r, j - 1, j >= 1, ot);
         load_qp(r, min(j + 1, nc - 1));
         load_vg(r, min(j + 3, nc - 1));
+        out_store(ot, j - 1, j >= 1);
       } else {
         load_vg(r, min(j + 3, nc - 1));
-        output(r, j - 1, j >= 1);
+        if constexpr (SAVE) save_chunk(j - 1, j >= 1);
       }
       __syncthreads();
     };
@@ -556,15 +518,20 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     if (j < nc) step(j, rB);
     if (nc > 0) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-      output((nc - 1) & 1 ? rB : rA, nc - 1, true);
+      if constexpr (OUT) {
+        out_form((nc - 1) & 1 ? rB : rA, nc - 1, true, ot);
+        out_store(ot, nc - 1, true);
+      } else if constexpr (SAVE) {
+        save_chunk(nc - 1, true);
+      }
     }
   }
 }
 
 template <int K, bool SAVE, bool OUT>
-void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* h0,
-                     float* ht, uint16_t* o, const int32_t* cu, int N, int T, int total,
-                     int Hqk, int Hv, int V, float scale, const ChunkWs& ws, hipStream_t st) {
+void launch_chain_sw(const uint16_t* v, const float* h0, float* ht, uint16_t* o,
+                     const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
+                     float scale, const ChunkWs& ws, hipStream_t st) {
   // two V tiles per workgroup once the chains fill the GPU twice over: the
   // tiles share the stage and output waves' operand traffic, and every chain
   // still has a state wave of its own (not with both outputs: a fifth wave
@@ -573,37 +540,24 @@ void launch_chain_sw(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
   constexpr int kExtra = SAVE && OUT ? 1 : 0;
   if (!(SAVE && OUT) && V % 32 == 0 && chains >= 2LL * device_cus())
     hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT, (SAVE && OUT) ? 1 : 2>),
-                       dim3((unsigned)(chains / 2)), dim3((4 + kExtra) * 64), 0, st, q, k, v, h0,
-                       ht, o, cu, N, T, total, Hqk, Hv, V, scale, ws);
+                       dim3((unsigned)(chains / 2)), dim3((4 + kExtra) * 64), 0, st, v, h0, ht,
+                       o, cu, N, T, total, Hqk, Hv, V, scale, ws);
   else
     hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT, 1>), dim3((unsigned)chains),
-                       dim3((3 + kExtra) * 64), 0, st, q, k, v, h0, ht, o, cu, N, T, total, Hqk,
-                       Hv, V, scale, ws);
+                       dim3((3 + kExtra) * 64), 0, st, v, h0, ht, o, cu, N, T, total, Hqk, Hv,
+                       V, scale, ws);
 }
 
-template void launch_chain_sw<64, false, true>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                                 const float*, float*, uint16_t*, const int32_t*, int,
-                                                 int, int, int, int, int, float, const ChunkWs&,
-                                                 hipStream_t);
-template void launch_chain_sw<64, true, false>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                                 const float*, float*, uint16_t*, const int32_t*, int,
-                                                 int, int, int, int, int, float, const ChunkWs&,
-                                                 hipStream_t);
-template void launch_chain_sw<64, true, true>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                                 const float*, float*, uint16_t*, const int32_t*, int,
-                                                 int, int, int, int, int, float, const ChunkWs&,
-                                                 hipStream_t);
-template void launch_chain_sw<128, false, true>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                                 const float*, float*, uint16_t*, const int32_t*, int,
-                                                 int, int, int, int, int, float, const ChunkWs&,
-                                                 hipStream_t);
-template void launch_chain_sw<128, true, false>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                                 const float*, float*, uint16_t*, const int32_t*, int,
-                                                 int, int, int, int, int, float, const ChunkWs&,
-                                                 hipStream_t);
-template void launch_chain_sw<128, true, true>(const uint16_t*, const uint16_t*, const uint16_t*,
-                                                 const float*, float*, uint16_t*, const int32_t*, int,
-                                                 int, int, int, int, int, float, const ChunkWs&,
-                                                 hipStream_t);
+#define GDN_CHAIN_INST(K_, SAVE_, OUT_)                                                       \
+  template void launch_chain_sw<K_, SAVE_, OUT_>(const uint16_t*, const float*, float*,     \
+                                                 uint16_t*, const int32_t*, int, int, int, int, \
+                                                 int, int, float, const ChunkWs&, hipStream_t);
+GDN_CHAIN_INST(64, false, true)
+GDN_CHAIN_INST(64, true, false)
+GDN_CHAIN_INST(64, true, true)
+GDN_CHAIN_INST(128, false, true)
+GDN_CHAIN_INST(128, true, false)
+GDN_CHAIN_INST(128, true, true)
+#undef GDN_CHAIN_INST
 
 }  // namespace gdn

@@ -70,6 +70,35 @@ __device__ __forceinline__ f32x4 mfma16(u16x8 a, u16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(a), as_bf(b), c, 0, 0, 0);
 }
 
+// fp16 forms (the prefill chain's state products): fp32 -> fp16 rounds to
+// nearest even, two values per v_cvt_pk_f16_f32 on gfx950.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+__device__ __forceinline__ u16x4 f2h4(f32x4 x) {
+  return __builtin_bit_cast(u16x4, __builtin_convertvector(x, f16x4));
+}
+// eight bf16 values as fp16 (exact for |x| in fp16's normal range)
+__device__ __forceinline__ u16x8 bf2h8(u16x8 x) {
+  const f32x8 f = __builtin_convertvector(__builtin_bit_cast(bf16x8, x), f32x8);
+  return __builtin_bit_cast(u16x8, __builtin_convertvector(f, f16x8));
+}
+// eight fp16 values re-rounded to bf16 (for the backward's bf16 saves)
+__device__ __forceinline__ u16x8 h2bf8(u16x8 x) {
+  const f32x8 f = __builtin_convertvector(__builtin_bit_cast(f16x8, x), f32x8);
+  return __builtin_bit_cast(u16x8, __builtin_convertvector(f, bf16x8));
+}
+
+// D += A(16x32) * B(32x16), fp16 operands, fp32 accumulate (same fragment
+// layouts as mfma16).
+__device__ __forceinline__ f32x4 mfma16h(u16x8 a, u16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
 // D = A B + C for fp32 16x16x4 (one block): lane l holds A[l % 16][l / 16]
 // and B[l / 16][l % 16]; D has the same layout as the 16x16x32 bf16 form.
 __device__ __forceinline__ f32x4 mfma4f32(float a, float b, f32x4 c) {

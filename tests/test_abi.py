@@ -142,9 +142,16 @@ def test_workspace_bytes_grow_with_problem(lib):
     b = f(1, 16384, 16, 32, 128, 128, 1, 0, 0)
     c = f(1, 8192, 16, 32, 128, 128, 64, 1, 0)
     d = f(1, 8192, 16, 32, 128, 128, 1, 0, 1)
-    assert 0 < a < b and c > a and d > a
-    # per (chunk, v-head): 64 gate floats (G) + 16 KiB Tb + 8 KiB P fragments
-    assert a >= 128 * 32 * (256 + 16384 + 8192)
+    # in-kernel l2norm needs no more forward workspace: the chain reads the
+    # prep kernel's fp16 copies of K and Q either way
+    assert 0 < a < b and c > a and d == a
+    # per (chunk, v-head): 64 gate floats (G) + 6 KiB Tb + 6 KiB P fragments;
+    # per (chunk, qk-head): the fp16 K block (18 KiB with its LDS padding)
+    # and the fp16 Q fragments (16 KiB)
+    assert a >= 128 * 32 * (256 + 6144 + 6144) + 128 * 16 * (18432 + 16384)
+    # the backward's workspace keeps the normalised rows with l2norm
+    bw = lib.gdn_chunk_bwd_workspace_bytes
+    assert bw(1, 8192, 16, 32, 128, 128, 1, 0, 1) > bw(1, 8192, 16, 32, 128, 128, 1, 0, 0)
 
 
 def test_empty_problem_is_a_noop(lib):

@@ -296,9 +296,10 @@ def test_prefill_deterministic(rocm_device):
 
 def test_prefill_homogeneous_cfg1(rocm_device):
     """Config 1 in full, no oracle: the recurrence is jointly linear in (h0, v), and every step
-    of the kernels commutes with doubling (bf16 hi/lo splits, MFMA products and fp32 sums of
-    doubled operands are the doubled results), so doubling h0 and v doubles o and the final state
-    bit for bit."""
+    of the kernels commutes with doubling (fp16 roundings, MFMA products and fp32 sums of doubled
+    operands are the doubled results) except where an fp16 operand falls below fp16's normal
+    range (|x| < 2^-14), whose rounding step is absolute (2^-24).  So doubling h0 and v doubles
+    the final state to ~1e-7 and o to within one bf16 rounding."""
     from avelang_amd import chunk_gated_delta_rule
     t = W.config("cfg1_prefill_qwen3next", seed=21).torch(rocm_device)
     o1, s1 = chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
@@ -306,8 +307,9 @@ def test_prefill_homogeneous_cfg1(rocm_device):
     o2, s2 = chunk_gated_delta_rule(t["q"], t["k"], 2 * t["v"], t["g"], t["beta"],
                                     initial_state=2 * t["initial_state"], output_final_state=True)
     torch.cuda.synchronize()
-    assert torch.equal(o2, 2 * o1)
-    assert torch.equal(s2, 2 * s1)
+    fro = ((s2 - 2 * s1).norm() / (2 * s1).norm()).item()
+    assert fro < 1e-5, fro
+    torch.testing.assert_close(o2.float(), 2 * o1.float(), rtol=2 ** -7, atol=1e-5)
 
 
 def test_prefill_beta_zero_pure_decay_cfg1(rocm_device):
