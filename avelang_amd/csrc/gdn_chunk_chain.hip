@@ -133,7 +133,10 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     auto step = [&](auto b3c) {
       constexpr int b3 = decltype(b3c)::value;
       const unsigned char* Kb = Kst[b3];
-      // operands of the step, all from LDS and issued first
+      // operands of the step, all from LDS and issued first, in the order
+      // they are used (e^G_last first: the state's decay may be scheduled
+      // early)
+      const float egl = Egl[b3];
       u16x8 ka[KB][4], ta[6];
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
@@ -143,18 +146,23 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       }
 #pragma unroll
       for (int i = 0; i < 6; ++i) ta[i] = Tst[b3][i][lane];
-      f32x4 eg[4], dc[4], vv[4];
+      // V at tokens rho(16 ti + 4 grp + r) = r0 + r, column r16: one
+      // transposing read of the 4 token rows per tile (widened to fp32 only
+      // where Y is formed, so that no read waits on another's conversion)
+      f32x4 eg[4], dc[4];
+      u16x4 v4[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int r0 = 32 * (ti >> 1) + 8 * grp + 4 * (ti & 1);
+        v4[ti] = lds_tr16(&Vrw[b3][vs][r0 + (r16 >> 2)][4 * (r16 & 3)]);
+      }
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
         const int r0 = 32 * (ti >> 1) + 8 * grp + 4 * (ti & 1);
         eg[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][0][r0]);
         dc[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][1][r0]);
-        // V at tokens rho(16 ti + 4 grp + r) = r0 + r, column r16: one
-        // transposing read of the 4 token rows
-        const u16x4 v4 = lds_tr16(&Vrw[b3][vs][r0 + (r16 >> 2)][4 * (r16 & 3)]);
-        vv[ti] = f32x4{bf2f(v4[0]), bf2f(v4[1]), bf2f(v4[2]), bf2f(v4[3])};
       }
-      const float egl = Egl[b3];
+
 
       // X = K S on the four rho-ordered token tiles, k-block by k-block:
       // state tiles 2b, 2b+1 (rounded to fp16) feed k-block b
@@ -170,9 +178,12 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       }
       // Y = V - e^G X (B fragments) and vnew = Tb Y, k-block 0 first: row
       // tiles 0 and 1 of vnew are then complete
+      auto vf = [&](int ti) {
+        return f32x4{bf2f(v4[ti][0]), bf2f(v4[ti][1]), bf2f(v4[ti][2]), bf2f(v4[ti][3])};
+      };
       auto yfrag = [&](int b) {
-        return cat8(f2h4(vv[2 * b] - eg[2 * b] * X[2 * b]),
-                    f2h4(vv[2 * b + 1] - eg[2 * b + 1] * X[2 * b + 1]));
+        return cat8(f2h4(vf(2 * b) - eg[2 * b] * X[2 * b]),
+                    f2h4(vf(2 * b + 1) - eg[2 * b + 1] * X[2 * b + 1]));
       };
       f32x4 vn[4];
       {
