@@ -22,6 +22,12 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
+// A launch error already pending on this thread when an entry point starts
+// belongs to earlier work (another library's launch, say): it is taken off
+// the thread before this library's launches, so that check_launch reports
+// only the entry point's own.
+void launch_begin() { (void)hipGetLastError(); }
+
 int check_launch(const char* what) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {

@@ -632,6 +632,7 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const float* g,
                    float scale, int use_qk_l2norm, void* workspace, size_t workspace_bytes,
                    const gdn::GateIn& gate, void* stream, const char* name) {
   if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
+  gdn_host::launch_begin();
   const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
                                      use_qk_l2norm != 0, false);
   if (!workspace || workspace_bytes < p.total)
@@ -693,7 +694,7 @@ extern "C" int gdn_chunk_fwd_gating(const void* q, const void* k, const void* v,
 // Device scratch of gdn_chunk_fwd_noalloc: one array per GPU the library runs
 // on, held until the process ends.  Its name is a host-side stand-in: host
 // code uses the per-device address from hipGetSymbolAddress, never the name.
-constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+constexpr size_t kNoAllocScratchBytes = GDN_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
@@ -713,7 +714,12 @@ int scratch_address(void** out) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* ptr = nullptr;
+    // relaxed capture mode for this thread, so that a first call made under
+    // stream capture may look the symbol up (it enqueues nothing)
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const hipError_t me = hipThreadExchangeStreamCaptureMode(&mode);
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (me == hipSuccess) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || !ptr)
       return gdn_host::fail(e != hipSuccess ? static_cast<int>(e) : GDN_ERR_NULL,
                             std::string("gdn_chunk_fwd_noalloc: hipGetSymbolAddress: ") +
@@ -736,6 +742,7 @@ extern "C" int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v
                                      K, V, N);
   if (rc) return rc;
   if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
+  gdn_host::launch_begin();
   const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
                                      use_qk_l2norm != 0, false);
   if (p.total > kNoAllocScratchBytes)
@@ -766,6 +773,7 @@ extern "C" int gdn_chunk_fwd_save(const void* q, const void* k, const void* v, c
                                      K, V, N);
   if (rc) return rc;
   if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
+  gdn_host::launch_begin();
   const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
                                      use_qk_l2norm != 0, true);
   if (!workspace || workspace_bytes < p.total)

@@ -953,6 +953,7 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
     }
   }
   if (N == 0 || (tokens == 0 && !dh0)) return GDN_OK;
+  gdn_host::launch_begin();
   const gdn::WsPlan p = gdn::plan_ws(B, T, Hqk, Hv, K, V, N, cu_seqlens != nullptr,
                                      use_qk_l2norm != 0, true);
   if (!workspace || workspace_bytes < p.total)

@@ -268,6 +268,7 @@ __device__ __forceinline__ void gate_at(const GateIn& p, long long i, int h, flo
 namespace gdn_host {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
+void launch_begin();
 int check_launch(const char* what);
 // [a, a + na) and [b, b + nb) share a byte (callers skip NULL pointers).
 bool overlaps(const void* a, size_t na, const void* b, size_t nb);

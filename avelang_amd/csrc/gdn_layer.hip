@@ -517,6 +517,7 @@ extern "C" int gdn_gating_fwd(const void* A_log, const void* a, const void* b,
   if (!(sp_beta > 0.f)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_gating_fwd: softplus beta must be > 0");
   const long long n = rows * H;
   if (n == 0) return GDN_OK;
+  gdn_host::launch_begin();
   if (!A_log || !a || !dt_bias || !g || (beta && !b))
     return gdn_host::fail(GDN_ERR_NULL, "gdn_gating_fwd: A_log, a, dt_bias, g (and b with beta) must be non-NULL");
   const gdn::GateIn gp{A_log, a, beta ? b : nullptr, dt_bias, a_dtype, b_dtype, p_dtype, sp_beta,
@@ -533,6 +534,7 @@ extern "C" int gdn_l2norm_fwd(const void* x, void* y, long long rows, int D, flo
     return gdn_host::fail(GDN_ERR_SHAPE, "gdn_l2norm_fwd: D must be 64, 128 or 256");
   if (!dtype_ok(dtype)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_l2norm_fwd: unsupported dtype code");
   if (rows == 0) return GDN_OK;
+  gdn_host::launch_begin();
   if (!x || !y) return gdn_host::fail(GDN_ERR_NULL, "gdn_l2norm_fwd: x and y must be non-NULL");
   if (rows > (1LL << 36)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_l2norm_fwd: too many rows");
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16)
@@ -561,6 +563,7 @@ extern "C" int gdn_rmsnorm_gated_fwd(const void* x, const void* z, const void* w
   if (!dtype_ok(dtype) || !dtype_ok(w_dtype))
     return gdn_host::fail(GDN_ERR_SHAPE, "gdn_rmsnorm_gated_fwd: unsupported dtype code");
   if (rows == 0) return GDN_OK;
+  gdn_host::launch_begin();
   if (!x || !z || !weight || !out)
     return gdn_host::fail(GDN_ERR_NULL, "gdn_rmsnorm_gated_fwd: x, z, weight and out must be non-NULL");
   if (rows > (1LL << 36)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_rmsnorm_gated_fwd: too many rows");
@@ -638,6 +641,7 @@ extern "C" int gdn_causal_conv1d_fwd(const void* x, const void* weight, const vo
     return gdn_host::fail(GDN_ERR_SHAPE,
                           "gdn_causal_conv1d_fwd: seq_idx and initial_states cannot be combined");
   if ((long long)B * D == 0) return GDN_OK;
+  gdn_host::launch_begin();
   if (!weight || (T > 0 && (!x || !out)))
     return gdn_host::fail(GDN_ERR_NULL, "gdn_causal_conv1d_fwd: x, weight and out must be non-NULL");
   if ((long long)B * D * (long long)(T > 0 ? T : 1) > (1LL << 40) || D > (1 << 24))
@@ -677,6 +681,7 @@ extern "C" int gdn_causal_conv1d_update(const void* x, void* conv_state, const v
   if (!conv_state_indices && num_slots < B)
     return gdn_host::fail(GDN_ERR_SHAPE, "gdn_causal_conv1d_update: without indices num_slots must be >= B");
   if ((long long)B * D == 0) return GDN_OK;
+  gdn_host::launch_begin();
   if (!x || !conv_state || !weight || !out)
     return gdn_host::fail(GDN_ERR_NULL, "gdn_causal_conv1d_update: x, conv_state, weight and out must be non-NULL");
   if (B > 65535 || D > (1 << 24))

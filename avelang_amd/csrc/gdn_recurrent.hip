@@ -304,6 +304,7 @@ int recurrent_plain(const void* q, const void* k, const void* v, const float* g,
                     float scale, int use_qk_l2norm, const gdn::GateIn& gate, void* stream,
                     const char* name) {
   if (N == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;  // nothing to compute
+  gdn_host::launch_begin();
   auto* qq = static_cast<const uint16_t*>(q);
   auto* kk = static_cast<const uint16_t*>(k);
   auto* vv = static_cast<const uint16_t*>(v);
@@ -342,6 +343,7 @@ int recurrent_indexed(const void* q, const void* k, const void* v, const float* 
       return gdn_host::fail(GDN_ERR_ALIAS, std::string(name) + ": ht must equal h0 exactly or not overlap it");
   }
   if (N == 0 || num_slots == 0 || ((long long)B * T == 0 && !ht)) return GDN_OK;
+  gdn_host::launch_begin();
   auto* qq = static_cast<const uint16_t*>(q);
   auto* kk = static_cast<const uint16_t*>(k);
   auto* vv = static_cast<const uint16_t*>(v);
@@ -447,6 +449,7 @@ extern "C" int gdn_recurrent_fwd_spec(const void* q, const void* k, const void* 
   if (N > 0 && (!state_indices || !pool))
     return gdn_host::fail(GDN_ERR_NULL, "gdn_recurrent_fwd_spec: pool and state_indices must be non-NULL");
   if (N == 0 || num_slots == 0 || (long long)B * T == 0) return GDN_OK;
+  gdn_host::launch_begin();
   auto* qq = static_cast<const uint16_t*>(q);
   auto* kk = static_cast<const uint16_t*>(k);
   auto* vv = static_cast<const uint16_t*>(v);

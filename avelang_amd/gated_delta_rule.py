@@ -237,10 +237,13 @@ def chunk_gated_delta_rule_fwd_save(
     return o, ht, workspace
 
 
-# The autograd forward keeps the backward's workspace (chunk-start states,
-# deltas, the prep's fragments: ~82 KB per chunk and v-head, 672 MB for a
-# T = 8192, 32-head layer) alive until the backward, which then skips the
-# forward recomputation.  False: keep only the inputs and recompute.
+# Default of chunk_gated_delta_rule's save_for_backward: the autograd forward
+# keeps the backward's workspace (chunk_bwd_workspace_bytes: chunk-start
+# states, deltas, the prep's fragments and fp16 K / Q copies -- about 170 KB
+# per chunk and v-head, 701 MB for a T = 8192, 32-v-head layer) alive until
+# the backward, which then skips the forward recomputation.  False: keep
+# only the inputs and recompute (the backward then takes ~0.2 ms more at that
+# shape).
 SAVE_FORWARD_FOR_BACKWARD = True
 
 
@@ -250,9 +253,9 @@ class _ChunkGatedDeltaRule(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
-                use_qk_l2norm_in_kernel):
+                use_qk_l2norm_in_kernel, save_for_backward):
         ws = None
-        if SAVE_FORWARD_FOR_BACKWARD:
+        if save_for_backward:
             B, T, Hqk, K = q.shape
             Hv, V = v.shape[2], v.shape[3]
             N = B if cu_seqlens is None else cu_seqlens.numel() - 1
@@ -282,7 +285,7 @@ class _ChunkGatedDeltaRule(torch.autograd.Function):
             q, k, v, g, beta, do.to(torch.bfloat16), dht.float() if dht is not None else None,
             ctx.scale, h0, cu, ctx.l2, workspace=ws, saved=ws is not None)
         return (dq, dk, dv, dg.to(ctx.g_dtype), db.to(ctx.beta_dtype), None, dh0, None, None,
-                None)
+                None, None)
 
 
 def chunk_gated_delta_rule(
@@ -300,6 +303,7 @@ def chunk_gated_delta_rule(
     workspace: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
     final_state: Optional[torch.Tensor] = None,
+    save_for_backward: Optional[bool] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Chunked (C = 64) gated-delta-rule prefill on gfx950.
 
@@ -314,6 +318,11 @@ def chunk_gated_delta_rule(
     Differentiable: when any of q, k, v, g, beta, initial_state requires
     grad (and grad mode is on) the call goes through an autograd function
     whose backward is ``chunk_gated_delta_rule_bwd`` (gdn_chunk_bwd).
+    ``save_for_backward`` (default: the module's SAVE_FORWARD_FOR_BACKWARD)
+    chooses, for that call, between keeping the backward's workspace from
+    the forward (``chunk_bwd_workspace_bytes(...)`` bytes held until the
+    backward, 701 MB at T = 8192 with 32 v-heads; the backward skips the
+    recomputation) and keeping only the inputs (the backward recomputes).
     """
     if torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (q, k, v, g, beta, initial_state)):
@@ -322,9 +331,10 @@ def chunk_gated_delta_rule(
                              "are not supported when gradients are required.")
         if scale is None:
             scale = q.shape[-1] ** -0.5
+        save = SAVE_FORWARD_FOR_BACKWARD if save_for_backward is None else bool(save_for_backward)
         res = _ChunkGatedDeltaRule.apply(q, k, v, g, beta, float(scale), initial_state,
                                          bool(output_final_state), cu_seqlens,
-                                         bool(use_qk_l2norm_in_kernel))
+                                         bool(use_qk_l2norm_in_kernel), save)
         return (res[0], res[1]) if output_final_state else (res, None)
     return _chunk_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
                       use_qk_l2norm_in_kernel, workspace=workspace, out=out,

@@ -653,111 +653,6 @@ def _backward_record(bwd, no_cpu):
     }
 
 
-# One wave per CU of gfx950: what an MFMA (16x16x32 bf16) and an fp32 VALU
-# instruction cost when one wave issues them, and how much of the MFMA
-# time independent VALU work hides when the two are interleaved in program
-# order (sched_group_barrier) versus issued as bursts.  The chunk chain's
-# state wave runs alone on its SIMD, so these are its issue costs.
-_HW_PROBE_SRC = r"""
-#include <hip/hip_runtime.h>
-#include <stdio.h>
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-// MODE 0: 8 independent MFMAs per iteration; 1: NV independent fp32 FMAs;
-// 2: 8 x (1 MFMA, NV/8 FMAs) interleaved; 3: 8 MFMAs then NV FMAs.
-template <int MODE, int NV>
-__global__ __launch_bounds__(64) void probe(float* out, int iters, float s, double* cyc) {
-  bf16x8 a, b;
-  for (int i = 0; i < 8; ++i) { a[i] = (__bf16)(threadIdx.x * 0.001f + i); b[i] = (__bf16)(i * 0.5f); }
-  f32x4 acc[8];
-  for (int i = 0; i < 8; ++i) acc[i] = f32x4{0, 0, 0, 0};
-  float x[16];
-  for (int i = 0; i < 16; ++i) x[i] = threadIdx.x + i;
-  const long long t0 = __builtin_amdgcn_s_memtime();
-  for (int it = 0; it < iters; ++it) {
-    if (MODE == 0) {
-#pragma unroll
-      for (int m = 0; m < 8; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[m], 0, 0, 0);
-    } else if (MODE == 1) {
-#pragma unroll
-      for (int v = 0; v < NV; ++v) x[v % 16] = __builtin_fmaf(x[v % 16], s, 1.0f);
-    } else if (MODE == 2) {
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[m], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-#pragma unroll
-        for (int v = 0; v < NV / 8; ++v) x[(m * (NV / 8) + v) % 16] = __builtin_fmaf(x[(m * (NV / 8) + v) % 16], s, 1.0f);
-        __builtin_amdgcn_sched_group_barrier(0x002, NV / 8, 0);
-      }
-    } else {
-#pragma unroll
-      for (int m = 0; m < 8; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[m], 0, 0, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-#pragma unroll
-      for (int v = 0; v < NV; ++v) x[v % 16] = __builtin_fmaf(x[v % 16], s, 1.0f);
-      __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
-    }
-  }
-  const long long t1 = __builtin_amdgcn_s_memtime();
-  if (threadIdx.x == 0 && blockIdx.x == 0) cyc[0] = (double)(t1 - t0) / iters;
-  float r = 0;
-  for (int i = 0; i < 8; ++i) r += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
-  for (int i = 0; i < 16; ++i) r += x[i];
-  out[blockIdx.x * 64 + threadIdx.x] = r;
-}
-
-template <int MODE, int NV>
-static void run(const char* nm, float* out, double* dc, int ncu) {
-  probe<MODE, NV><<<ncu, 64>>>(out, 64, 0.999f, dc);
-  probe<MODE, NV><<<ncu, 64>>>(out, 4096, 0.999f, dc);
-  hipDeviceSynchronize();
-  double c;
-  hipMemcpy(&c, dc, 8, hipMemcpyDeviceToHost);
-  printf("{\"case\": \"%s\", \"mfma\": %d, \"valu\": %d, \"ticks_per_iteration\": %.1f}\n",
-         nm, MODE == 1 ? 0 : 8, MODE == 0 ? 0 : NV, c);
-}
-
-int main() {
-  hipDeviceProp_t p;
-  hipGetDeviceProperties(&p, 0);
-  float* out;
-  double* dc;
-  hipMalloc(&out, p.multiProcessorCount * 64 * 4);
-  hipMalloc(&dc, 8);
-  run<0, 0>("mfma only", out, dc, p.multiProcessorCount);
-  run<1, 32>("valu only", out, dc, p.multiProcessorCount);
-  run<1, 64>("valu only", out, dc, p.multiProcessorCount);
-  run<2, 32>("interleaved 1 mfma : 4 valu", out, dc, p.multiProcessorCount);
-  run<2, 64>("interleaved 1 mfma : 8 valu", out, dc, p.multiProcessorCount);
-  run<3, 32>("burst 8 mfma then 32 valu", out, dc, p.multiProcessorCount);
-  run<3, 64>("burst 8 mfma then 64 valu", out, dc, p.multiProcessorCount);
-  return 0;
-}
-"""
-
-
-def hw_probe():
-    """Compile and run _HW_PROBE_SRC (one JSON line per case; ticks are
-    s_memtime counts per loop iteration, one wave per CU)."""
-    import subprocess
-    import tempfile
-    from avelang_amd import build as B
-    with tempfile.TemporaryDirectory() as d:
-        src, exe = os.path.join(d, "probe.hip"), os.path.join(d, "probe")
-        with open(src, "w") as f:
-            f.write(_HW_PROBE_SRC)
-        flags = [f for f in B.HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
-        r = subprocess.run([B.hipcc(), *flags, src, "-o", exe], capture_output=True, text=True)
-        if r.returncode:
-            raise RuntimeError(r.stderr[-2000:])
-        r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
-        print(r.stdout, end="", flush=True)
-        if r.returncode:
-            raise RuntimeError(r.stderr[-2000:])
-
-
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -779,12 +674,7 @@ def main():
                     help="only the config-1 backward measurement (profiling runs)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic.json from two rocprofv3 --pmc runs of --profile-pass")
-    ap.add_argument("--hw-probe", action="store_true",
-                    help="MFMA / VALU issue costs of one wave and their overlap (compiles a probe)")
     args = ap.parse_args()
-    if args.hw_probe:
-        hw_probe()
-        return
     if args.pmc_table:
         pmc_table(args.pmc_table)
         return

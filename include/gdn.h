@@ -82,18 +82,27 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v,
 size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
                                  int N, int has_cu_seqlens, int use_qk_l2norm);
 
+/* Bytes of device scratch gdn_chunk_fwd_noalloc owns on every GPU. */
+#define GDN_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
 /*
  * gdn_chunk_fwd without a workspace argument: the library's own device
- * scratch (a fixed array of 32 MiB per GPU, held until the process ends)
+ * scratch (a fixed array of GDN_NOALLOC_SCRATCH_BYTES = 32 MiB per GPU)
  * takes its place, so the call allocates nothing -- no hipMalloc, no
  * hipFree, no allocating library routine.  No counterpart in the
  * reference; it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation).
- * Problems whose gdn_chunk_workspace_bytes(...) exceeds 32 MiB (about 1300
- * chunk x v-head pairs, e.g. T = 2048 at 32 v-heads) are rejected with
+ * The array is part of libgdn.so's device code object: every process that
+ * loads the library holds those 32 MiB on every GPU it uses, until it ends,
+ * whether or not it calls this entry point.
+ * Problems whose gdn_chunk_workspace_bytes(...) exceeds 32 MiB (about 2200
+ * tokens at 32 v-heads / 16 qk-heads, K = V = 128) are rejected with
  * GDN_ERR_WORKSPACE before anything is enqueued.  Every call on one GPU
  * shares that GPU's scratch: calls that overlap on one GPU (different
  * streams, or host threads) race and must be serialised by the caller.
+ * The scratch's device address is looked up on a device's first call
+ * (in relaxed stream-capture mode, so that first call may itself be under
+ * capture).
  */
 int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v,
                           const float* g, const float* beta,

@@ -18,6 +18,7 @@ BAD = {
     "decreasing": [0, 100, 50, 230],
     "short_total": [0, 70, 200],
     "nonzero_start": [5, 70, 230],
+    "overshoot": [0, 70, 300],
 }
 
 

@@ -256,6 +256,14 @@ def test_autograd_without_saved_forward(rocm_device, monkeypatch):
         grads.append([x.grad for x in leaves])
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+    # and per call, against the module default (True here)
+    t = wl.torch(rocm_device)
+    leaves = [t[n].clone().requires_grad_(True) for n in ("q", "k", "v", "g", "beta")]
+    o, _ = chunk_gated_delta_rule(*leaves, initial_state=t["initial_state"],
+                                  save_for_backward=False)
+    (o.float() * dO.float()).sum().backward()
+    for a, x in zip(grads[0], leaves):
+        assert torch.equal(a, x.grad)
 
 
 def test_bwd_varlen_many_sequences(rocm_device):

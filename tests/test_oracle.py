@@ -177,6 +177,29 @@ def test_l2norm_option_matches_prenormalised_inputs():
     np.testing.assert_allclose(S, S2, rtol=1e-12)
 
 
+def test_l2norm_eps_inside_the_square_root():
+    """R.l2norm against what the formula x / sqrt(|x|^2 + eps), eps = 1e-6, fixes at both
+    ends, with the norm from numpy.linalg.norm: a large-norm row comes out unit-norm, and a
+    row of norm 1e-5 (|x|^2 = 1e-10, negligible beside eps) is scaled by eps^-1/2 = 1000.
+    Planted mistakes fail: eps outside the square root (x / (|x| + eps) scales the tiny
+    row by ~9e4), eps dropped (unit norm for the tiny row), eps squared inside."""
+    rng = np.random.default_rng(31)
+    big = rng.standard_normal((3, 128)) * 7.0
+    tiny = rng.standard_normal((3, 128))
+    tiny *= 1e-5 / np.linalg.norm(tiny, axis=-1, keepdims=True)
+    nb = R.l2norm(big)
+    np.testing.assert_allclose(np.linalg.norm(nb, axis=-1), 1.0, rtol=1e-7)
+    np.testing.assert_allclose(nb, big / np.linalg.norm(big, axis=-1, keepdims=True), rtol=1e-7)
+    nt = R.l2norm(tiny)
+    np.testing.assert_allclose(nt, tiny * 1e3, rtol=1e-4)
+    np.testing.assert_allclose(np.linalg.norm(nt, axis=-1), 1e-2, rtol=1e-4)
+    mistakes = [lambda x: x / (np.linalg.norm(x, axis=-1, keepdims=True) + 1e-6),
+                lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True),
+                lambda x: x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-12)]
+    for bad in mistakes:
+        assert not np.allclose(bad(tiny), nt, rtol=1e-2)
+
+
 def test_default_scale_is_inverse_sqrt_k():
     a = _inputs(seed=11)
     o, _ = R.recurrent(**a)

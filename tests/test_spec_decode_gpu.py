@@ -127,3 +127,46 @@ def test_spec_padding_rows_untouched(rocm_device):
     torch.cuda.synchronize()
     assert (o[2] == 7.0).all()
     assert torch.equal(pool2[idx2[2].long()], before[idx2[2].long()])
+
+
+@pytest.mark.parametrize("Hqk,Hv,K,V", [(16, 32, 128, 128), (2, 4, 64, 64)])
+def test_spec_packed_drafts_of_mixed_length(rocm_device, Hqk, Hv, K, V):
+    """Packed drafts (cu_seqlens) of lengths 3, 0, 6, 1 with a slot row of S = 4: every slot
+    a token writes holds the oracle state after that prefix; the 6-token draft's tokens 5 and
+    6 (past the row) advance the state without writing any slot; the empty draft writes
+    nothing; every slot outside the written ones keeps its contents; o equals the oracle."""
+    lens = [3, 0, 6, 1]
+    N, S = len(lens), 4
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    wl = W.make(1, int(cu[-1]), Hqk, Hv, K, V, seed=61, h0_scale=0.01, cu_seqlens=cu)
+    a = wl.numpy()
+    dev = rocm_device
+    rng = np.random.Generator(np.random.PCG64(9))
+    nslots = 3 * N * S
+    idx = rng.permutation(nslots)[: N * S].astype(np.int32).reshape(N, S)
+    pool = 0.5 * torch.randn((nslots, Hv, K, V), device=dev)
+    pool[torch.from_numpy(idx[:, 0]).long().to(dev)] = torch.from_numpy(a["initial_state"]).to(dev)
+    before = pool.clone()
+    t = wl.torch(dev)
+    from avelang_amd import fused_recurrent_gated_delta_rule
+    o, p = fused_recurrent_gated_delta_rule(
+        t["q"], t["k"], t["v"], t["g"], t["beta"], initial_state=pool, output_final_state=True,
+        cu_seqlens=t["cu_seqlens"], ssm_state_indices=torch.from_numpy(idx).to(dev))
+    torch.cuda.synchronize()
+    assert p.data_ptr() == pool.data_ptr()
+    o_ref, _ = oracle.run("recurrent", **a)
+    err = np.abs(o.float().cpu().numpy() - o_ref)
+    assert (err <= O_TOL + O_TOL * np.abs(o_ref)).all(), f"o max err {err.max():.3e}"
+    pc, bc = pool.cpu().numpy(), before.cpu().numpy()
+    written = set()
+    for n, L in enumerate(lens):
+        seq = {key: a[key][:, cu[n]:cu[n + 1]] for key in ("q", "k", "v", "g", "beta")}
+        for tt in range(1, min(L, S) + 1):
+            _, s_ref = oracle.run("recurrent", **{key: val[:, :tt] for key, val in seq.items()},
+                                  initial_state=a["initial_state"][n:n + 1])
+            fro = _fro(pc[idx[n, tt - 1]][None], s_ref)
+            assert fro <= S_FRO, f"seq {n} state after token {tt}: rel fro {fro:.3e}"
+            written.add(int(idx[n, tt - 1]))
+    for sl in range(nslots):
+        if sl not in written:
+            assert np.array_equal(pc[sl], bc[sl]), f"slot {sl} changed"
