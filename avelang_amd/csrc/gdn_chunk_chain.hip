@@ -9,15 +9,19 @@
 //       X = K S,  Y = V - e^G X,  vnew = Tb Y,
 //       S = e^G_last S + K^T (e^(G_last - G) vnew)
 //   (Tb = (I + A)^-1 diag(beta) from the prep kernel; K S, Tb Y and K^T U
-//   as hi + lo bf16 MFMA products).  Each product's result tile is the next
+//   as single fp16 MFMA products of operands rounded from fp32, which keeps
+//   the final state within ~4e-4 relative Frobenius of the exact chain at
+//   any length).  Each product's result tile is the next
 //   product's B operand where it stands (row orders below), so no LDS
 //   exchange sits inside the step, and every operand comes from LDS.
 //
-//   the stage wave loads chunk c+2's K rows and Tb fragments straight into
-//   LDS (buffer_load ... lds) while step c runs.
+//   the stage wave loads chunk c+2's K rows (the prep kernel's fp16 copy,
+//   already in this kernel's LDS layout), Tb fragments (already in rho row
+//   order) and V tiles straight into LDS (buffer_load ... lds) while step c
+//   runs.
 //
-//   the output wave writes chunk c+1's V tiles (as fp32, in the state
-//   waves' layout) and gate factors into LDS and forms chunk c-1's output
+//   the output wave writes chunk c+1's gate factors into LDS and forms chunk
+//   c-1's output
 //   from the state and vnew fragments the state waves leave in LDS:
 //       o = scale e^G (Q S) + P vnew
 //   (with both the backward's saves and o, a save wave stores the former).
@@ -32,7 +36,7 @@
 // so a lane's rows of tiles 2b and 2b + 1 are exactly the natural indices
 // 32 b + 8 grp + i of k-block b.  The state's key rows and the token rows of
 // X, Y and vnew use rho; K, Q, P and the columns of Tb stay in natural
-// order (the Tb fragments are gathered by rho-permuted row).
+// order (the prep writes the Tb fragments by rho-permuted row).
 #include <type_traits>
 
 #include "gdn_chunk.h"
@@ -309,10 +313,9 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     }
   } else {
     // ----------------------------------------------------- output wave ----
-    // During step j: writes chunk j+1's V tile (as fp32, in the state wave's
-    // layout) and gate factors into stage buffer (j+1) % 3, forms chunk
-    // j-1's output, then loads chunk j+1's Q rows and P fragments and chunk
-    // j+3's V tile and G into registers.  A register set is loaded two
+    // During step j: writes chunk j+1's gate factors into stage buffer
+    // (j+1) % 3, forms chunk j-1's output, then loads chunk j+1's Q and P
+    // fragments and chunk j+3's G into registers.  A register set is loaded two
     // steps before it is used (two sets, the loop unrolled by two), and
     // every step issues the same loads and stores, so each wait names an
     // exact count.

@@ -314,6 +314,9 @@ def chunk_gated_delta_rule(
     to avoid allocation; ``final_state`` may be ``initial_state`` itself.
     With ``use_qk_l2norm_in_kernel`` q and k are L2-normalised (eps 1e-6)
     and rounded to bf16 before use, as FLA's separate l2norm pass does.
+    The sequential state products run on fp16 operands (fp32 state and
+    accumulation): q, k and v must stay inside fp16's range, which
+    l2-normalised q / k and a layer's v do by orders of magnitude.
 
     Differentiable: when any of q, k, v, g, beta, initial_state requires
     grad (and grad mode is on) the call goes through an autograd function
