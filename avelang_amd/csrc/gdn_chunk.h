@@ -30,11 +30,14 @@ struct ChunkWs {
   float* tmat;      // [NC][Hv][10][16][16] T = (I + A)^-1 (fp32): its lower 16 x 16
                     // blocks (rt, cb), cb <= rt, in the order tmat_block() gives,
                     // each row-major (the diagonal blocks' upper part 0)
-  u16x8* ttfrag;    // [NC][Hv][4][2][2][64] A-operand fragments of Tb^T (hi, lo)
-  u16x8* ptfrag;    // [NC][Hv][4][2][64]    A-operand fragments of P^T
-                    // (both: row tiles 2, 3 of k-block 0 are zero and left unwritten)
-  u16x8* qtfrag;    // [NC][Hqk][K/16][2][64] A-operand fragments of Q^T (key-row tile,
-                    // token k-block; the l2-normalised q with use_qk_l2norm)
+  // (the three below: rows in the reverse chain's rho order, so that each
+  // (tile, k-block) fragment is one contiguous 1 KiB block)
+  u16x8* ttfrag;    // [NC][Hv][6][64] fp16 A-operand fragments of Tb^T, slot
+                    // tb_slot(row tile, k-block)
+  u16x8* ptfrag;    // [NC][Hv][4][2][64] bf16 A-operand fragments of P^T
+                    // (both: row tiles 2, 3 of k-block 0 are zero, P^T's left unwritten)
+  u16x8* qtfrag;    // [NC][Hqk][K/16][2][64] fp16 A-operand fragments of Q^T (key-row
+                    // tile, token k-block; the l2-normalised q with use_qk_l2norm)
   uint16_t* hs;     // [NC][Hv][V][K] bf16: state at the start of every chunk, transposed
   uint16_t* dl;     // [B*T][Hv][V]   bf16: d = vnew, the per-token delta
 };
@@ -198,9 +201,9 @@ void launch_chain_sw(const uint16_t* v, const float* h0, float* ht, uint16_t* o,
                      float scale, const ChunkWs& ws, hipStream_t st);
 
 // Reverse chain of the backward (gdn_chunk_rev.hip): dS' of every chunk into
-// dse, dd into dd, dh0.
+// dse, dd into dd, dh0 (K rows from ws.k16).
 template <int K>
-void launch_rev_sw(const uint16_t* k, const uint16_t* dO, const float* dht, float* dh0,
+void launch_rev_sw(const uint16_t* dO, const float* dht, float* dh0,
                    const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
                    float scale, const ChunkWs& ws, uint16_t* dse, uint16_t* dd, hipStream_t st);
 

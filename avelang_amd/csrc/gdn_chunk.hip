@@ -361,21 +361,26 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   __syncthreads();
 
   if constexpr (BWD) {
-    // A-operand fragments of Q^T for the reverse chain (key-row tile T,
-    // token k-block b; lane (r16, grp) holds Q[32 b + 8 grp + i][16 T + r16]),
-    // once per qk-head: the chunk's Q rows pass through the K staging space,
-    // free after K K^T, and each wave gathers key-row tiles w, w + 4, ...
+    // fp16 A-operand fragments of Q^T for the reverse chain, in its rho row
+    // order: natural key row R = 16 T + r16 is row m = 4 ((R / 8) % 4) + R % 4
+    // of rho tile t = 2 (R / 32) + (R / 4) % 2, and lane m + 16 grp of
+    // (t, token k-block b) holds Q[32 b + 8 grp + i][R].  Once per qk-head:
+    // the chunk's Q rows pass through the K staging space, free after K K^T,
+    // and each wave gathers natural key-row tiles w, w + 4, ...
     if (h % (Hv / Hqk) == 0) {
 #pragma unroll
       for (int b = 0; b < KB; ++b)
         *reinterpret_cast<u16x8*>(&Ks[16 * w + r16][32 * b + 8 * grp]) = qa[b];
       __syncthreads();
       const size_t qb = ((size_t)ci * Hqk + hq) * (K / 16);
+      const int m = 4 * (2 * (w & 1) + (r16 >> 3)) + (r16 & 3);
 #pragma unroll
       for (int T = w; T < K / 16; T += 4) {
+        const int t = 2 * (T >> 1) + ((r16 >> 2) & 1);
 #pragma unroll
         for (int b = 0; b < 2; ++b)
-          ws.qtfrag[((qb + T) * 2 + b) * 64 + lane] = lds_colfrag(&Ks[0][0], K + 8, 32 * b, 16 * T, lane);
+          ws.qtfrag[((qb + t) * 2 + b) * 64 + m + 16 * grp] =
+              bf2h8(lds_colfrag(&Ks[0][0], K + 8, 32 * b, 16 * T, lane));
       }
       __syncthreads();
     }
@@ -435,7 +440,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   // natural row R = 16 w + r16 is row m = 4 ((R / 8) % 4) + R % 4 of rho
   // tile ti = 2 (R / 32) + (R / 4) % 2; lane m + 16 grp of slot tb_slot(ti, b)
   // holds k = 32 b + 8 grp .. + 7
-  const size_t base = ((size_t)ci * Hv + h) * 4 + w;
   const int row = 16 * w + r16;
   {
     const int ti = 2 * (w >> 1) + ((r16 >> 2) & 1);
@@ -459,28 +463,29 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     }
   }
   if constexpr (BWD) {
-    // Tb^T fragments, row tile w: Tb^T[m][kk] = T[kk][m] beta_m (kk >= m);
-    // k-block 0 of row tiles 2 and 3 is zero (in Tb^T and P^T) and never
-    // read: not stored
+    // Tb^T (fp16) and P^T (bf16) A-operand fragments in the reverse chain's
+    // rho row order (natural row m = 16 w + r16 as for Tb above): Tb^T[m][kk]
+    // = T[kk][m] beta_m (kk >= m) in slot tb_slot(ti, b), P^T[m][kk] =
+    // P[kk][m] in slot 2 ti + b; k-block 0 of rho tiles 2 and 3 (natural rows
+    // 32..63) is zero in both and never read: not stored
     const int m = 16 * w + r16;
     const float bm = Bs[m];
+    const int ti = 2 * (w >> 1) + ((r16 >> 2) & 1);
+    const int mr = 4 * (2 * (w & 1) + (r16 >> 3)) + (r16 & 3) + 16 * grp;
+    u16x8* ttd = ws.ttfrag + ((size_t)ci * Hv + h) * 6 * 64 + mr;
+    u16x8* ptd = ws.ptfrag + (((size_t)ci * Hv + h) * 4 + ti) * 2 * 64 + mr;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       if (b == 0 && w >= 2) continue;
-      u16x8 th, tl;
+      f32x4 x0, x1;
 #pragma unroll
-      for (int ii = 0; ii < 8; ++ii) {
+      for (int ii = 0; ii < 4; ++ii) {
         const int kk = 32 * b + 8 * grp + ii;
-        const float x = kk >= m ? Tm[kk * kLdA + m] * bm : 0.f;
-        uint16_t xh, xl;
-        split_bf(x, xh, xl);
-        th[ii] = xh;
-        tl[ii] = xl;
+        x0[ii] = kk >= m ? Tm[kk * kLdA + m] * bm : 0.f;
+        x1[ii] = kk + 4 >= m ? Tm[(kk + 4) * kLdA + m] * bm : 0.f;
       }
-      ws.ttfrag[((base * 2 + b) * 2 + 0) * 64 + lane] = th;
-      ws.ttfrag[((base * 2 + b) * 2 + 1) * 64 + lane] = tl;
-      // P^T fragments: P^T[m][kk] = P[kk][m]
-      ws.ptfrag[(base * 2 + b) * 64 + lane] = lds_colfrag(&Ps[0][0], 72, 32 * b, 16 * w, lane);
+      ttd[tb_slot(ti, b) * 64] = cat8(f2h4(x0), f2h4(x1));
+      ptd[b * 64] = lds_colfrag(&Ps[0][0], 72, 32 * b, 16 * w, lane);
     }
     // T itself, fp32, its lower blocks only: wave w stores blocks (w, 0..w)
     // of its row tile, one contiguous 1 KB block per store (the diagonal
@@ -523,7 +528,7 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
   }
   if (bwd) {
     p.tmat = take(nch * kTPacked * 4);
-    p.ttfrag = take(nch * 4 * 2 * 2 * 64 * 16);
+    p.ttfrag = take(nch * 6 * 64 * 16);
     p.ptfrag = take(nch * 4 * 2 * 64 * 16);
     p.hs = take(nch * K * V * 2);
     p.dse = take(nch * K * V * 2);

@@ -894,7 +894,7 @@ static void launch_bwd_kernels(const uint16_t* q, const uint16_t* k, const uint1
   ws.dse = reinterpret_cast<uint16_t*>(wsb + p.dse);
   ws.dd = reinterpret_cast<uint16_t*>(wsb + p.dd);
   const int total = B * T;
-  launch_rev_sw<K>(kn, dO, dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws.f, ws.dse, ws.dd, st);
+  launch_rev_sw<K>(dO, dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws.f, ws.dse, ws.dd, st);
   if (p.ncmax > 0) {
     // one resident workgroup per CU (the kernel's LDS allows no second),
     // each taking every grid-th (chunk, qk-head) item

@@ -11,14 +11,16 @@
 // waves in place of its output wave:
 //
 //   wave 0, the state wave, holds every key row of the tile's dS' in VGPRs
-//   (rho row order) and runs the dS'-dependent products alone: K dS' (hi +
-//   lo), Tb^T dd (three hi / lo terms), K^T U (hi + lo), every operand from
+//   (rho row order) and runs the dS'-dependent products alone: K dS',
+//   Tb^T dd and K^T U, each one v_mfma_f32_16x16x32_f16 pass with fp16
+//   operands rounded from fp32 (as the forward chain), every operand from
 //   LDS and every result tile the next product's B operand where it stands.
 //   The terms that do not depend on dS' -- P^T dO and Q^T (c' e^G dO) -- it
 //   reads as fp32 tiles in its own layout.
 //
-//   wave 1, the stage wave, loads the K rows and Tb^T fragments of the chunk
-//   two steps ahead straight into LDS (buffer_load ... lds).
+//   wave 1, the stage wave, copies the chunk's fp16 K block and Tb^T
+//   fragments two steps ahead straight into LDS (buffer_load ... lds), both
+//   contiguous as the prep kernel laid them out.
 //
 //   waves 2 and 3, the helper waves, form the next step's gate factors and
 //   P^T dO (wave 2) and Q^T (c' e^G dO) (wave 3) from the prep's P^T and
@@ -34,23 +36,24 @@ namespace gdn {
 
 template <int K>
 __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
-    const uint16_t* __restrict__ k, const uint16_t* __restrict__ dO, const float* dht,
+    const uint16_t* __restrict__ dO, const float* dht,
     float* dh0, const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
     float scale, ChunkWs ws, uint16_t* __restrict__ dse, uint16_t* __restrict__ ddo) {
   constexpr int KB = K / 32;   // k-blocks over the key index
   constexpr int ST = K / 16;   // 16-row state tiles
   using KL = KLayout<K>;
-  // stage buffers (step j in buffer j % 3): K rows, Tb^T fragments by rho row
+  // stage buffers (step j in buffer j % 3): fp16 K rows (KLayout), Tb^T
+  // fragments (rho rows)
   __shared__ __attribute__((aligned(16))) unsigned char Kst[3][KL::BYTES];
-  __shared__ __attribute__((aligned(16))) u16x8 Tst[3][6][2][64];
+  __shared__ __attribute__((aligned(16))) u16x8 Tst[3][6][64];
   // helper -> state: e^G and e^(G_last - G) by token, e^G_last, P^T dO
   // (token tiles in the state wave's layout) and Q^T (c' e^G dO) (state tiles)
   __shared__ __attribute__((aligned(16))) float Gst[3][2][64];
   __shared__ float Egl[3];
   __shared__ __attribute__((aligned(16))) f32x4 Pst[3][4][64];
   __shared__ __attribute__((aligned(16))) f32x4 Qst[3][ST][64];
-  // state -> helper: dS' hi B fragments at the step's start, dd (bf16) as B
-  // fragments
+  // state -> helper: dS' (bf16) B fragments at the step's start, dd (bf16)
+  // as B fragments
   __shared__ __attribute__((aligned(16))) u16x8 Sx[3][KB][64];
   __shared__ __attribute__((aligned(16))) u16x8 Vx[3][2][64];
 
@@ -104,7 +107,10 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
     auto step = [&](auto b3c) {
       constexpr int b3 = decltype(b3c)::value;
       const unsigned char* Kb = Kst[b3];
-      u16x8 ka[KB][4], ta[6][2];
+      // operands of the step, all from LDS and issued first, in the order
+      // they are used
+      const float egl = Egl[b3];
+      u16x8 ka[KB][4], ta[6];
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
 #pragma unroll
@@ -112,10 +118,7 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
           ka[b][ti] = *reinterpret_cast<const u16x8*>(Kb + ka_off[ti] + 64 * b);
       }
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        ta[i][0] = Tst[b3][i][0][lane];
-        ta[i][1] = Tst[b3][i][1][lane];
-      }
+      for (int i = 0; i < 6; ++i) ta[i] = Tst[b3][i][lane];
       f32x4 eg[4], dc[4], pd[4];
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
@@ -124,48 +127,34 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         dc[ti] = *reinterpret_cast<const f32x4*>(&Gst[b3][1][r0]);
         pd[ti] = Pst[b3][ti][lane];
       }
-      const float egl = Egl[b3];
 
-      // X = K dS' on the rho-ordered token tiles (dS' hi also to the helper)
+      // X = K dS' on the rho-ordered token tiles: state tiles 2b, 2b+1
+      // (rounded to fp16) feed k-block b; dS' as bf16 to the helper's save
       f32x4 X[4];
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) X[ti] = zero4();
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
-        u16x4 h0v, l0v, h1v, l1v;
-        split_bf4(S[2 * b], h0v, l0v);
-        split_bf4(S[2 * b + 1], h1v, l1v);
-        const u16x8 sh = cat8(h0v, h1v), sl = cat8(l0v, l1v);
-        Sx[b3][b][lane] = sh;
+        const u16x8 sh = cat8(f2h4(S[2 * b]), f2h4(S[2 * b + 1]));
+        Sx[b3][b][lane] = cat8(f2bf4(S[2 * b]), f2bf4(S[2 * b + 1]));
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sh, X[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16(ka[b][ti], sl, X[ti]);
+        for (int ti = 0; ti < 4; ++ti) X[ti] = mfma16h(ka[b][ti], sh, X[ti]);
       }
-      // dd = P^T dO + e^(G_L - G) X on token tiles 2b, 2b + 1 (hi, lo B
-      // fragments of k-block b of Tb^T dd; hi also stored as dd)
-      auto ddsplit = [&](int b, u16x8& yh, u16x8& yl) {
-        u16x4 hh0, ll0, hh1, ll1;
-        split_bf4(pd[2 * b] + dc[2 * b] * X[2 * b], hh0, ll0);
-        split_bf4(pd[2 * b + 1] + dc[2 * b + 1] * X[2 * b + 1], hh1, ll1);
-        yh = cat8(hh0, hh1);
-        yl = cat8(ll0, ll1);
-        Vx[b3][b][lane] = yh;
+      // dd = P^T dO + e^(G_L - G) X on token tiles 2b, 2b + 1: the fp16 B
+      // fragment of k-block b of Tb^T dd, and dd (bf16) for the save
+      auto ddfrag = [&](int b) {
+        const f32x4 d0 = pd[2 * b] + dc[2 * b] * X[2 * b];
+        const f32x4 d1 = pd[2 * b + 1] + dc[2 * b + 1] * X[2 * b + 1];
+        Vx[b3][b][lane] = cat8(f2bf4(d0), f2bf4(d1));
+        return cat8(f2h4(d0), f2h4(d1));
       };
       // Z = Tb^T dd: Tb^T is upper triangular, so token tiles 2 and 3 have
       // no k-block 0; k-block 1 first, where every tile has a term
       f32x4 z[4];
-#pragma unroll
-      for (int ti = 0; ti < 4; ++ti) z[ti] = zero4();
       {
-        u16x8 yh, yl;
-        ddsplit(1, yh, yl);
+        const u16x8 y1 = ddfrag(1);
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 1)][0], yh, z[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 1)][0], yl, z[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 1)][1], yh, z[ti]);
+        for (int ti = 0; ti < 4; ++ti) z[ti] = mfma16h(ta[tb_slot(ti, 1)], y1, zero4());
       }
       u16x8 kt[2][ST];
 #pragma unroll
@@ -179,28 +168,18 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         }
       }
       {
-        u16x8 yh, yl;
-        ddsplit(0, yh, yl);
+        const u16x8 y0 = ddfrag(0);
 #pragma unroll
-        for (int ti = 0; ti < 2; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 0)][0], yh, z[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 2; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 0)][0], yl, z[ti]);
-#pragma unroll
-        for (int ti = 0; ti < 2; ++ti) z[ti] = mfma16(ta[tb_slot(ti, 0)][1], yh, z[ti]);
+        for (int ti = 0; ti < 2; ++ti) z[ti] = mfma16h(ta[tb_slot(ti, 0)], y0, z[ti]);
       }
       // dS = e^G_L dS' + Q^T (c' e^G dO) + K^T U,  U = -e^G Z, block by block
 #pragma unroll
       for (int t = 0; t < ST; ++t) S[t] = S[t] * egl + Qst[b3][t][lane];
 #pragma unroll
       for (int b = 1; b >= 0; --b) {
-        u16x4 hh0, ll0, hh1, ll1;
-        split_bf4(-(eg[2 * b] * z[2 * b]), hh0, ll0);
-        split_bf4(-(eg[2 * b + 1] * z[2 * b + 1]), hh1, ll1);
-        const u16x8 uh = cat8(hh0, hh1), ul = cat8(ll0, ll1);
+        const u16x8 uh = cat8(f2h4(-(eg[2 * b] * z[2 * b])), f2h4(-(eg[2 * b + 1] * z[2 * b + 1])));
 #pragma unroll
-        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], uh, S[t]);
-#pragma unroll
-        for (int t = 0; t < ST; ++t) S[t] = mfma16(kt[b][t], ul, S[t]);
+        for (int t = 0; t < ST; ++t) S[t] = mfma16h(kt[b][t], uh, S[t]);
       }
       __syncthreads();   // step j's outputs published; stage buffer j % 3 free
     };
@@ -224,44 +203,26 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
     }
   } else if (w == 1) {
     // ------------------------------------------------------ stage wave ----
-    // As in the forward chain: step j + 2's K rows and Tb^T fragments
-    // straight to LDS during step j, bare barriers, explicit waits.
+    // As in the forward chain: step j + 2's fp16 K block (KLayout, rows
+    // past the sequence end zero) and Tb^T fragments (rho rows) straight to
+    // LDS during step j, lane l of load i copying bytes 16 (64 i + l) of the
+    // contiguous source; bare barriers, explicit waits.
     typedef __attribute__((address_space(3))) void* lds_ptr;
-    constexpr int P = K / 8;
-    constexpr int kKT = KL::LOADS + 12;
-    const int rowq = Hqk * K * 2;
+    constexpr int kKT = KL::LOADS + 6;
     auto issue_kt = [&](int j, int jb) {
-      const int jc = nc - 1 - j;
-      const int ci = c_begin + jc, buf = jb % 3;
-      const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
+      const int ci = c_begin + nc - 1 - j, buf = jb % 3;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(k + ((size_t)t0 * Hqk + hq) * K), 0, L * rowq, kBufferFlags);
+          ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES, 0, KL::BYTES, kBufferFlags);
 #pragma unroll
-      for (int i = 0; i < KL::LOADS; ++i) {
-        const int p = 64 * i + lane;
-        const int g16 = p / KL::GU, rem = p % KL::GU;
-        const int row = 16 * g16 + rem / (KL::RS / 16), piece = rem % (KL::RS / 16);
-        const bool data = rem < 16 * (KL::RS / 16) && piece < P && p < KL::UNITS;
+      for (int i = 0; i < KL::LOADS; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(Kst[buf] + 1024 * i), 16,
-                                                 data ? row * rowq + 16 * piece : 0x7ffffff0,
-                                                 0, 0, 0);
-      }
-      // Tb^T fragments gathered by rho row (token tiles 2, 3 have no k-block 0)
+                                                 1024 * i + 16 * lane, 0, 0, 0);
       const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
-          ws.ttfrag + ((size_t)ci * Hv + h) * 4 * 256, 0, 4 * 256 * 16, kBufferFlags);
+          ws.ttfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-        const int row = rho_row(ti, r16);
-        const int src = (row >> 4) * 256 + (row & 15) + 16 * grp;
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          if (b == 0 && ti >= 2) continue;
-#pragma unroll
-          for (int hl = 0; hl < 2; ++hl)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr)&Tst[buf][tb_slot(ti, b)][hl][0],
-                                                     16, (src + 128 * b + 64 * hl) * 16, 0, 0, 0);
-        }
-      }
+      for (int i = 0; i < 6; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr)&Tst[buf][i][0], 16,
+                                                 1024 * i + 16 * lane, 0, 0, 0);
     };
     auto barrier = [] {
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -292,8 +253,8 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
       constexpr bool qwave = decltype(qwc)::value;
       constexpr int kStep = qwave ? 2 * ST + 16 + 1 : 6 + 16 + 1 + KB + 2;
       struct Regs {
-        u16x8 pt[6];        // P^T fragments (rho rows) by tb_slot (wave 2)
-        u16x8 qt[ST][2];    // Q^T fragments (rho key rows) by token k-block (wave 3)
+        u16x8 pt[6];        // P^T fragments (rho rows, bf16) by tb_slot (wave 2)
+        u16x8 qt[ST][2];    // Q^T fragments (rho key rows, fp16) by token k-block (wave 3)
         u16x8 dof[2];       // dO[32 kb + 8 grp + i][16 vt + r16] (B operand)
         float G;            // G of token `lane`
       };
@@ -307,25 +268,21 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
               ws.qtfrag + ((size_t)ci * Hqk + hq) * ST * 128, 0, ST * 128 * 16, kBufferFlags);
 #pragma unroll
           for (int t = 0; t < ST; ++t) {
-            const int row = rho_row(t, r16);
-            const int src = (row >> 4) * 128 + (row & 15) + 16 * grp;
 #pragma unroll
             for (int b = 0; b < 2; ++b)
               r.qt[t][b] = __builtin_bit_cast(
-                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, (src + 64 * b) * 16, 0, 0));
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((2 * t + b) * 64 + lane) * 16, 0, 0));
           }
         } else {
           const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
               ws.ptfrag + ((size_t)ci * Hv + h) * 4 * 128, 0, 4 * 128 * 16, kBufferFlags);
 #pragma unroll
           for (int ti = 0; ti < 4; ++ti) {
-            const int row = rho_row(ti, r16);
-            const int src = (row >> 4) * 128 + (row & 15) + 16 * grp;
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
               if (b == 0 && ti >= 2) continue;
               r.pt[tb_slot(ti, b)] = __builtin_bit_cast(
-                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (src + 64 * b) * 16, 0, 0));
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, ((2 * ti + b) * 64 + lane) * 16, 0, 0));
             }
           }
         }
@@ -350,8 +307,8 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         const int buf = j % 3;
         const float eg = __expf(r.G);
         if constexpr (qwave) {
-          // c' e^G dO for this lane's k-slots (tokens 32 kb + 8 grp + i), hi + lo
-          u16x8 oh[2], ol[2];
+          // c' e^G dO for this lane's k-slots (tokens 32 kb + 8 grp + i), fp16
+          u16x8 oh[2];
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) {
             f32x4 x0, x1;
@@ -363,21 +320,14 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
               x0[i] = scale * e0 * bf2f(r.dof[kb][i]);
               x1[i] = scale * e1 * bf2f(r.dof[kb][4 + i]);
             }
-            u16x4 h0v, l0v, h1v, l1v;
-            split_bf4(x0, h0v, l0v);
-            split_bf4(x1, h1v, l1v);
-            oh[kb] = cat8(h0v, h1v);
-            ol[kb] = cat8(l0v, l1v);
+            oh[kb] = cat8(f2h4(x0), f2h4(x1));
           }
 #pragma unroll
           for (int t = 0; t < ST; ++t) {
-            f32x4 a = zero4(), b = zero4();
+            f32x4 a = zero4();
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-              a = mfma16(r.qt[t][kb], oh[kb], a);
-              b = mfma16(r.qt[t][kb], ol[kb], b);
-            }
-            Qst[buf][t][lane] = a + b;
+            for (int kb = 0; kb < 2; ++kb) a = mfma16h(r.qt[t][kb], oh[kb], a);
+            Qst[buf][t][lane] = a;
           }
         } else {
           const int jc = nc - 1 - j;
@@ -474,18 +424,18 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
 }
 
 template <int K>
-void launch_rev_sw(const uint16_t* k, const uint16_t* dO, const float* dht, float* dh0,
-                   const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
-                   float scale, const ChunkWs& ws, uint16_t* dse, uint16_t* dd, hipStream_t st) {
-  hipLaunchKernelGGL((chunk_rev_sw_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, k, dO,
+void launch_rev_sw(const uint16_t* dO, const float* dht, float* dh0, const int32_t* cu, int N,
+                   int T, int total, int Hqk, int Hv, int V, float scale, const ChunkWs& ws,
+                   uint16_t* dse, uint16_t* dd, hipStream_t st) {
+  hipLaunchKernelGGL((chunk_rev_sw_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, dO,
                      dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws, dse, dd);
 }
 
-template void launch_rev_sw<64>(const uint16_t*, const uint16_t*, const float*, float*,
-                                const int32_t*, int, int, int, int, int, int, float,
-                                const ChunkWs&, uint16_t*, uint16_t*, hipStream_t);
-template void launch_rev_sw<128>(const uint16_t*, const uint16_t*, const float*, float*,
-                                 const int32_t*, int, int, int, int, int, int, float,
-                                 const ChunkWs&, uint16_t*, uint16_t*, hipStream_t);
+template void launch_rev_sw<64>(const uint16_t*, const float*, float*, const int32_t*, int, int,
+                                int, int, int, int, float, const ChunkWs&, uint16_t*, uint16_t*,
+                                hipStream_t);
+template void launch_rev_sw<128>(const uint16_t*, const float*, float*, const int32_t*, int, int,
+                                 int, int, int, int, float, const ChunkWs&, uint16_t*, uint16_t*,
+                                 hipStream_t);
 
 }  // namespace gdn

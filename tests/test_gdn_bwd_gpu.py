@@ -181,14 +181,20 @@ def test_autograd_matches_bwd(rocm_device):
 
 def test_bwd_linear_in_output_gradients(rocm_device):
     """No oracle: the gradients are linear in (dO, dht), and every step of the backward commutes
-    with doubling (bf16 hi/lo splits, MFMA products and fp32 sums of doubled operands), so
-    doubling dO and dht doubles every gradient bit for bit (config 1's heads, T = 1000)."""
+    with doubling (fp16 and bf16 roundings, MFMA products and fp32 sums of doubled operands are
+    the doubled results) except where an fp16 operand of the reverse chain falls below fp16's
+    normal range (|x| < 2^-14, an absolute rounding step of 2^-24).  So doubling dO and dht
+    doubles dh0 (fp32, straight from the reverse chain) to ~1e-6 and the other gradients, formed
+    from the chain's bf16 saves, to within a bf16 rounding (config 1's heads, T = 1000)."""
     wl = W.make(1, 1000, 16, 32, 128, 128, seed=31, h0_scale=0.01)
     do, dht = _grad_inputs(wl, 31)
     a = _gpu_bwd(wl, do, dht, rocm_device)
     b = _gpu_bwd(wl, 2 * do, 2 * dht, rocm_device)
     for name in a:
-        assert torch.equal(b[name], 2 * a[name]), name
+        want = 2 * a[name].float()
+        fro = ((b[name].float() - want).norm() / want.norm()).item()
+        print(f"doubling {name}: relative Frobenius deviation {fro:.2e}", flush=True)
+        assert fro < (1e-5 if name == "dh0" else 2 ** -8), (name, fro)
 
 
 def test_bwd_deterministic(rocm_device):
