@@ -7,8 +7,8 @@ Operators (FLA / Qwen3-Next argument lists):
                                       optionally over a pool of state slots
 
 Neighbours of the core in the Qwen3-Next layer (``layer_ops``):
-    fused_gdn_gating, l2norm_fwd, causal_conv1d_fn, causal_conv1d_update,
-    rms_norm_gated
+    fused_gdn_gating (differentiable; fused_gdn_gating_bwd), l2norm_fwd,
+    causal_conv1d_fn, causal_conv1d_update, rms_norm_gated
 
 All call hand-written HIP kernels through the C ABI in include/gdn.h and
 include/gdn_layer.h (``libgdn.so``, built by ``python -m avelang_amd.build``).
@@ -27,6 +27,7 @@ from .layer_ops import (  # noqa: F401
     causal_conv1d_fn,
     causal_conv1d_update,
     fused_gdn_gating,
+    fused_gdn_gating_bwd,
     l2norm_fwd,
     rms_norm_gated,
 )
@@ -41,6 +42,7 @@ __all__ = [
     "chunk_workspace_bytes",
     "chunk_bwd_workspace_bytes",
     "fused_gdn_gating",
+    "fused_gdn_gating_bwd",
     "l2norm_fwd",
     "causal_conv1d_fn",
     "causal_conv1d_update",

@@ -31,6 +31,8 @@ EXPORTS = (
     "gdn_recurrent_fwd_gating",
     # include/gdn_layer.h
     "gdn_gating_fwd",
+    "gdn_gating_bwd",
+    "gdn_gating_bwd_workspace_bytes",
     "gdn_l2norm_fwd",
     "gdn_causal_conv1d_fwd",
     "gdn_causal_conv1d_update",
@@ -129,6 +131,15 @@ def lib():
             _vp, _vp, _vp, _vp, _vp, _vp,     # A_log a b dt_bias g beta
             _ll, _i, _i, _i, _i,              # rows H a_dtype b_dtype p_dtype
             _f, _f, _vp,                      # softplus beta, threshold, stream
+        ]
+        h.gdn_gating_bwd_workspace_bytes.restype = _sz
+        h.gdn_gating_bwd_workspace_bytes.argtypes = [_ll, _i]
+        h.gdn_gating_bwd.restype = _i
+        h.gdn_gating_bwd.argtypes = [
+            _vp, _vp, _vp, _vp, _vp, _vp,     # A_log a b dt_bias dg dbeta
+            _vp, _vp, _vp, _vp,               # dA_log da db ddt_bias
+            _ll, _i, _i, _i, _i,              # rows H a_dtype b_dtype p_dtype
+            _f, _f, _vp, _sz, _vp,            # softplus beta, threshold, ws, ws bytes, stream
         ]
         h.gdn_l2norm_fwd.restype = _i
         h.gdn_l2norm_fwd.argtypes = [_vp, _vp, _ll, _i, _f, _i, _vp]

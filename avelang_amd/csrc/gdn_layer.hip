@@ -81,6 +81,84 @@ __global__ __launch_bounds__(256) void gating_kernel(GateIn p, float* g, float* 
   }
 }
 
+// ---------------------------------------------------- gating backward ----
+// Gradients of the gating (autograd of TF:650-652) from dg, dbeta:
+//   da = dg * -exp(A_log[h]) * softplus'(a + dt_bias[h]),  softplus'(x) =
+//        sigmoid(spb x), or 1 where spb x > spt (torch's softplus backward);
+//   db = dbeta * beta (1 - beta)  (formed as e^-|b| / (1 + e^-|b|)^2);
+//   ddt_bias[h] = sum over rows of da (fp32, before da is rounded to a's type),
+//   dA_log[h]   = sum over rows of dg * g   (d(-exp(A)) / dA = -exp(A)).
+// Deterministic sums: block blk takes rows [blk R, blk R + R); thread j of
+// head h (tph = 256 / H threads per head, consecutive threads consecutive
+// heads, so a row's elements are one coalesced access) sums rows j, j + tph,
+// .. in order, then the tph partials are summed in order and stored per
+// block; gating_bwd_reduce_kernel sums the block partials in order.
+__device__ __forceinline__ void st_dt(void* p, long long i, int dt, float v) {
+  if (dt == GDN_DTYPE_F32) static_cast<float*>(p)[i] = v;
+  else if (dt == GDN_DTYPE_BF16) ste<GDN_DTYPE_BF16>(p, i, v);
+  else ste<GDN_DTYPE_F16>(p, i, v);
+}
+__global__ __launch_bounds__(256) void gating_bwd_kernel(GateIn p, const float* __restrict__ dg,
+                                                         const float* __restrict__ dbeta, void* da,
+                                                         void* db, float* __restrict__ part,
+                                                         long long rows, int H, int R) {
+  __shared__ float red[2][256];
+  const int tph = 256 / H;
+  const int t = threadIdx.x, h = t % H, j = t / H;
+  const long long r0 = (long long)blockIdx.x * R;
+  const long long r1 = min(rows, r0 + R);
+  float sdt = 0.f, sA = 0.f;
+  if (j < tph) {
+    float neg_a, dtb;
+    gate_head(p, h, neg_a, dtb);
+    for (long long r = r0 + j; r < r1; r += tph) {
+      const long long i = r * H + h;
+      const float av = ldp(p.a, i, p.adt);
+      float g, unused;
+      gate_math(p, neg_a, dtb, av, 0.f, g, unused);
+      const float bx = p.spb * (av + dtb);
+      const float ex = expf(fminf(bx, p.spt));
+      const float dsp = bx > p.spt ? 1.f : ex / (1.f + ex);
+      const float dgi = dg[i];
+      const float dai = dgi * neg_a * dsp;
+      st_dt(da, i, p.adt, dai);
+      sdt += dai;
+      sA += dgi * g;
+      if (db) {
+        // beta (1 - beta) = e^-|b| / (1 + e^-|b|)^2, without the cancellation
+        // of 1 - beta where beta is near 1
+        const float eb = expf(-fabsf(ldp(p.b, i, p.bdt)));
+        st_dt(db, i, p.bdt, dbeta[i] * (eb / ((1.f + eb) * (1.f + eb))));
+      }
+    }
+  }
+  red[0][t] = sdt;
+  red[1][t] = sA;
+  __syncthreads();
+  if (t < H) {
+    float s0 = 0.f, s1 = 0.f;
+    for (int jj = 0; jj < tph; ++jj) {
+      s0 += red[0][jj * H + t];
+      s1 += red[1][jj * H + t];
+    }
+    part[((size_t)blockIdx.x * H + t) * 2] = s0;
+    part[((size_t)blockIdx.x * H + t) * 2 + 1] = s1;
+  }
+}
+__global__ __launch_bounds__(256) void gating_bwd_reduce_kernel(const float* __restrict__ part,
+                                                                int nblk, int H, void* dA_log,
+                                                                void* ddt, int pdt) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= H) return;
+  float s0 = 0.f, s1 = 0.f;
+  for (int b = 0; b < nblk; ++b) {
+    s0 += part[((size_t)b * H + h) * 2];
+    s1 += part[((size_t)b * H + h) * 2 + 1];
+  }
+  if (ddt) st_dt(ddt, h, pdt, s0);
+  if (dA_log) st_dt(dA_log, h, pdt, s1);
+}
+
 // Row kernels (l2norm, gated norm): a row of D elements is held by D / VEC
 // lanes with one 16-byte access each (LPR lanes per row, 64 / LPR rows per
 // wavefront), the row sum is a xor-shuffle over those lanes.
@@ -525,6 +603,58 @@ extern "C" int gdn_gating_fwd(const void* A_log, const void* a, const void* b,
   hipLaunchKernelGGL(gdn::gating_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), gp, g, beta, n, H);
   return gdn_host::check_launch("gdn_gating_fwd");
+}
+
+// rows per block of the gating backward: 64, more when that would leave
+// over 1024 block partials to sum
+static int gating_bwd_rows(long long rows) {
+  const long long r = (rows + 1023) / 1024;
+  return (int)(r < 64 ? 64 : r);
+}
+static long long gating_bwd_blocks(long long rows) {
+  const int R = gating_bwd_rows(rows);
+  return (rows + R - 1) / R;
+}
+
+extern "C" size_t gdn_gating_bwd_workspace_bytes(long long rows, int H) {
+  if (rows < 0 || H <= 0) return 0;
+  return (size_t)gating_bwd_blocks(rows) * (size_t)H * 2 * sizeof(float);
+}
+
+extern "C" int gdn_gating_bwd(const void* A_log, const void* a, const void* b,
+                              const void* dt_bias, const float* dg, const float* dbeta,
+                              void* dA_log, void* da, void* db, void* ddt_bias, long long rows,
+                              int H, int a_dtype, int b_dtype, int p_dtype, float sp_beta,
+                              float sp_threshold, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (rows < 0 || H <= 0 || H > 256)
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_gating_bwd: rows >= 0 and 0 < H <= 256");
+  if (!dtype_ok(a_dtype) || !dtype_ok(b_dtype) || !dtype_ok(p_dtype))
+    return gdn_host::fail(GDN_ERR_SHAPE, "gdn_gating_bwd: unsupported dtype code");
+  if (!(sp_beta > 0.f)) return gdn_host::fail(GDN_ERR_SHAPE, "gdn_gating_bwd: softplus beta must be > 0");
+  if (!A_log || !dt_bias || (rows > 0 && (!a || !dg || !da)))
+    return gdn_host::fail(GDN_ERR_NULL, "gdn_gating_bwd: A_log, dt_bias, a, dg and da must be non-NULL");
+  if ((db != nullptr) != (dbeta != nullptr) || (db && rows > 0 && !b))
+    return gdn_host::fail(GDN_ERR_NULL, "gdn_gating_bwd: db and dbeta go together, and need b");
+  const long long nblk = gating_bwd_blocks(rows);
+  const size_t need = gdn_gating_bwd_workspace_bytes(rows, H);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return gdn_host::fail(GDN_ERR_WORKSPACE, "gdn_gating_bwd: workspace NULL or smaller than "
+                                             "gdn_gating_bwd_workspace_bytes(rows, H)");
+  if (!dA_log && !ddt_bias && rows == 0) return GDN_OK;
+  gdn_host::launch_begin();
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  if (rows > 0) {
+    const gdn::GateIn gp{A_log, a, b, dt_bias, a_dtype, b_dtype, p_dtype, sp_beta, sp_threshold,
+                         rows * H, H};
+    hipLaunchKernelGGL(gdn::gating_bwd_kernel, dim3((unsigned)nblk), dim3(256), 0, st, gp, dg,
+                       dbeta, da, db, part, rows, H, gating_bwd_rows(rows));
+  }
+  if (dA_log || ddt_bias)
+    hipLaunchKernelGGL(gdn::gating_bwd_reduce_kernel, dim3((H + 255) / 256), dim3(256), 0, st,
+                       part, (int)nblk, H, dA_log, ddt_bias, p_dtype);
+  return gdn_host::check_launch("gdn_gating_bwd");
 }
 
 extern "C" int gdn_l2norm_fwd(const void* x, void* y, long long rows, int D, float eps,

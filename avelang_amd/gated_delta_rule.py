@@ -24,6 +24,7 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from . import _native
+from .layer_ops import fused_gdn_gating
 
 __all__ = [
     "chunk_gated_delta_rule",
@@ -622,6 +623,7 @@ def chunk_gated_delta_rule_gated(
     *,
     workspace: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
+    save_for_backward: Optional[bool] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """``chunk_gated_delta_rule`` with the layer's gating fused in.
 
@@ -631,8 +633,26 @@ def chunk_gated_delta_rule_gated(
     itself from ``a``, ``b`` ([B, T, Hv], bf16 / fp16 / fp32) and ``A_log``,
     ``dt_bias`` ([Hv]) -- the same definition as ``fused_gdn_gating``, so the
     result equals ``chunk_gated_delta_rule(q, k, v, *fused_gdn_gating(...))``
-    bit for bit -- and no fp32 g / beta tensor exists.  Forward only.
+    bit for bit -- and no fp32 g / beta tensor exists.
+
+    Differentiable: when any of q, k, v, a, b, A_log, dt_bias, initial_state
+    requires grad (and grad mode is on) the call is exactly that composition
+    under autograd -- ``fused_gdn_gating`` (its backward one kernel,
+    ``fused_gdn_gating_bwd``: da, db and the per-head sums of dA_log and
+    ddt_bias) feeding ``chunk_gated_delta_rule`` (backward gdn_chunk_bwd);
+    g and beta (fp32, 4 bytes per token and v-head each) are then held for
+    the backward.  ``save_for_backward`` as for ``chunk_gated_delta_rule``.
     """
+    if torch.is_grad_enabled() and any(
+            isinstance(t, torch.Tensor) and t.requires_grad
+            for t in (q, k, v, a, b, A_log, dt_bias, initial_state)):
+        if out is not None or workspace is not None:
+            raise ValueError("chunk_gated_delta_rule_gated: out / workspace buffers are not "
+                             "supported when gradients are required.")
+        g, beta = fused_gdn_gating(A_log, a, b, dt_bias, softplus_beta, softplus_threshold)
+        return chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state,
+                                      output_final_state, cu_seqlens, use_qk_l2norm_in_kernel,
+                                      save_for_backward=save_for_backward)
     return _chunk_fwd(q, k, v, a, b, scale, initial_state, output_final_state, cu_seqlens,
                       use_qk_l2norm_in_kernel, workspace=workspace, out=out,
                       gate=(A_log, dt_bias, softplus_beta, softplus_threshold),

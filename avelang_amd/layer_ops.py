@@ -7,6 +7,7 @@ RMSNorm.  These operators are those neighbours, with the argument lists of
 the kernel libraries the layer binds to:
 
     fused_gdn_gating        g, beta from (A_log, a, b, dt_bias)     TF:650-652
+                            (differentiable: fused_gdn_gating_bwd)
     l2norm_fwd              row L2 normalisation                     TF:368-371
     causal_conv1d_fn        prefill convolution (+ SiLU)             TF:346-365
     causal_conv1d_update    decode convolution, state in place       TF:326-343
@@ -30,6 +31,7 @@ from . import _native
 
 __all__ = [
     "fused_gdn_gating",
+    "fused_gdn_gating_bwd",
     "l2norm_fwd",
     "causal_conv1d_fn",
     "causal_conv1d_update",
@@ -94,8 +96,19 @@ def fused_gdn_gating(
     head axis last).  ``beta`` / ``threshold`` are softplus's parameters.
     The layer text evaluates ``b.sigmoid()`` in ``b``'s own dtype; here it
     is kept in fp32 (a difference below one bf16 ulp of beta).
+
+    Differentiable: when any input requires grad (and grad mode is on) the
+    backward is ``fused_gdn_gating_bwd`` (one kernel for da, db and the
+    per-head sums of dA_log and ddt_bias).
     """
-    name = "fused_gdn_gating"
+    if torch.is_grad_enabled() and any(
+            isinstance(t, torch.Tensor) and t.requires_grad for t in (A_log, a, b, dt_bias)):
+        return _GdnGating.apply(A_log, a, b, dt_bias, float(beta), float(threshold))
+    return _gating_fwd(A_log, a, b, dt_bias, beta, threshold)
+
+
+def _gating_args(A_log, a, b, dt_bias, beta, name):
+    """Validated, contiguous (A_log, a, b, dt_bias) and their dtype codes."""
     for nm, t in (("A_log", A_log), ("a", a), ("b", b), ("dt_bias", dt_bias)):
         if not isinstance(t, torch.Tensor):
             raise ValueError(f"{name}: {nm} must be a torch.Tensor")
@@ -110,9 +123,16 @@ def fused_gdn_gating(
     if not beta > 0:
         raise ValueError(f"{name}: softplus beta must be > 0.")
     adt, bdt, pdt = _dt(a, name, "a"), _dt(b, name, "b"), _dt(A_log, name, "A_log")
-    dev = a.device
-    _on(dev, name, b=b, A_log=A_log, dt_bias=dt_bias)
+    _on(a.device, name, b=b, A_log=A_log, dt_bias=dt_bias)
     a, b, A_log, dt_bias = (t.contiguous() for t in (a, b, A_log, dt_bias))
+    return A_log, a, b, dt_bias, adt, bdt, pdt
+
+
+def _gating_fwd(A_log, a, b, dt_bias, beta, threshold):
+    name = "fused_gdn_gating"
+    A_log, a, b, dt_bias, adt, bdt, pdt = _gating_args(A_log, a, b, dt_bias, beta, name)
+    H = a.shape[-1]
+    dev = a.device
     g = torch.empty(a.shape, dtype=torch.float32, device=dev)
     beta_out = torch.empty(a.shape, dtype=torch.float32, device=dev)
     rows = a.numel() // H
@@ -121,6 +141,74 @@ def fused_gdn_gating(
         beta_out.data_ptr(), rows, H, adt, bdt, pdt, float(beta), float(threshold), _stream(dev))
     _native.check(rc, name)
     return g, beta_out
+
+
+def fused_gdn_gating_bwd(
+    A_log: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    dt_bias: torch.Tensor,
+    dg: torch.Tensor,
+    dbeta: Optional[torch.Tensor] = None,
+    beta: float = 1.0,
+    threshold: float = 20.0,
+) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
+    """Gradients of ``fused_gdn_gating`` (autograd of TF:650-652) given
+    ``dg`` / ``dbeta`` (``a``'s shape): ``(dA_log, da, db, ddt_bias)``.
+
+    ``da = dg * -exp(A_log) * softplus'(a + dt_bias)`` and ``db = dbeta *
+    beta * (1 - beta)`` in ``a``'s / ``b``'s dtype; ``ddt_bias`` (the fp32
+    sum of da over every leading axis) and ``dA_log`` (that of ``dg * g``)
+    in the parameters' dtype, summed in a fixed order (deterministic).
+    ``softplus'`` is torch's: ``sigmoid(beta x)``, 1 above the threshold.
+    ``db`` is None when ``dbeta`` is.
+    """
+    name = "fused_gdn_gating_bwd"
+    A_log, a, b, dt_bias, adt, bdt, pdt = _gating_args(A_log, a, b, dt_bias, beta, name)
+    H = a.shape[-1]
+    dev = a.device
+    for nm, t in (("dg", dg), ("dbeta", dbeta)):
+        if t is not None and (not isinstance(t, torch.Tensor) or t.shape != a.shape
+                              or t.device != dev):
+            raise ValueError(f"{name}: {nm} must be a tensor of shape {tuple(a.shape)} on {dev}.")
+    dg = dg.float().contiguous()
+    dbeta = dbeta.float().contiguous() if dbeta is not None else None
+    rows = a.numel() // H
+    da = torch.empty_like(a)
+    db = torch.empty_like(b) if dbeta is not None else None
+    dA_log = torch.empty_like(A_log)
+    ddt = torch.empty_like(dt_bias)
+    lib = _native.lib()
+    nbytes = lib.gdn_gating_bwd_workspace_bytes(rows, H)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    rc = lib.gdn_gating_bwd(
+        A_log.data_ptr(), a.data_ptr(), b.data_ptr(), dt_bias.data_ptr(), dg.data_ptr(),
+        _ptr(dbeta), dA_log.data_ptr(), da.data_ptr(), _ptr(db), ddt.data_ptr(), rows, H,
+        adt, bdt, pdt, float(beta), float(threshold), ws.data_ptr(), nbytes, _stream(dev))
+    _native.check(rc, name)
+    return dA_log, da, db, ddt
+
+
+class _GdnGating(torch.autograd.Function):
+    """Autograd form of fused_gdn_gating: forward gdn_gating_fwd, backward
+    gdn_gating_bwd."""
+
+    @staticmethod
+    def forward(ctx, A_log, a, b, dt_bias, beta, threshold):
+        g, beta_out = _gating_fwd(A_log, a, b, dt_bias, beta, threshold)
+        ctx.save_for_backward(A_log, a, b, dt_bias)
+        ctx.sp = (beta, threshold)
+        return g, beta_out
+
+    @staticmethod
+    def backward(ctx, dg, dbeta):
+        A_log, a, b, dt_bias = ctx.saved_tensors
+        if dg is None:
+            dg = torch.zeros(a.shape, dtype=torch.float32, device=a.device)
+        dA_log, da, db, ddt = fused_gdn_gating_bwd(A_log, a, b, dt_bias, dg, dbeta, *ctx.sp)
+        if db is None:
+            db = torch.zeros_like(b)
+        return dA_log, da, db, ddt, None, None
 
 
 def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6,

@@ -45,6 +45,30 @@ int gdn_gating_fwd(const void* A_log, const void* a, const void* b, const void* 
                    float sp_beta, float sp_threshold, void* stream);
 
 /*
+ * Backward of gdn_gating_fwd: what autograd through the layer's gating
+ * expression (TF:650-652) gives, in one elementwise pass plus a per-head
+ * sum.  From dg, dbeta [rows, H] fp32 (the core's gradients w.r.t. g, beta):
+ *   da       [rows, H] (a_dtype) = dg * -exp(A_log) * softplus'(a + dt_bias)
+ *   db       [rows, H] (b_dtype) = dbeta * beta * (1 - beta)
+ *   ddt_bias [H] (p_dtype)       = sum over rows of da (fp32, before rounding)
+ *   dA_log   [H] (p_dtype)       = sum over rows of dg * g
+ * softplus'(x) = sigmoid(sp_beta x), or 1 where sp_beta x > sp_threshold
+ * (torch's softplus backward).  db / dbeta are nullable together; dA_log
+ * and ddt_bias are nullable.  The sums are deterministic (a fixed order, no
+ * atomics).  workspace: gdn_gating_bwd_workspace_bytes(rows, H) bytes of
+ * device memory (0 bytes: may be NULL).  0 < H <= 256.  No counterpart in
+ * the reference (it has no GDN code); the layer's autograd is what it
+ * replaces.
+ */
+size_t gdn_gating_bwd_workspace_bytes(long long rows, int H);
+int gdn_gating_bwd(const void* A_log, const void* a, const void* b, const void* dt_bias,
+                   const float* dg, const float* dbeta,
+                   void* dA_log, void* da, void* db, void* ddt_bias,
+                   long long rows, int H, int a_dtype, int b_dtype, int p_dtype,
+                   float sp_beta, float sp_threshold,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Row L2 normalisation, y = x * rsqrt(sum(x^2) + eps) over D (TF:368-371).
  *   x, y [rows, D] contiguous, same dtype (f32 / bf16 / f16); D in {64, 128, 256}.
  * y may equal x.

@@ -7,6 +7,7 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 Semantics follow transformers' Qwen3-Next layer text
 (models/qwen3_next/modeling_qwen3_next.py, 5.15.0, read as text):
     gating                 :650-652   g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
+    gating_bwd             autograd of :650-652 (torch's softplus backward)
     l2norm                 :368-371   (in gdn_ref)
     causal_conv1d          :346-365   depthwise conv over time, zero left padding, SiLU
     causal_conv1d_update   :326-343   conv over concat(state, x), state <- last S inputs
@@ -25,6 +26,7 @@ __all__ = [
     "bf16_round",
     "f16_round",
     "gating",
+    "gating_bwd",
     "causal_conv1d",
     "causal_conv1d_update",
     "rmsnorm_gated",
@@ -68,6 +70,26 @@ def gating(A_log, a, b, dt_bias, sp_beta=1.0, threshold=20.0):
     g = -np.exp(A_log) * sp
     beta = 1.0 / (1.0 + np.exp(-b))
     return g, beta
+
+
+def gating_bwd(A_log, a, b, dt_bias, dg, dbeta, sp_beta=1.0, threshold=20.0):
+    """Gradients of ``gating``'s (g, beta) w.r.t. (A_log, a, b, dt_bias) given
+    dg, dbeta (a's shape, head axis last), float64: (dA_log, da, db, ddt_bias).
+
+    d softplus(x) / dx = sigmoid(sp_beta x), or 1 where sp_beta x > threshold
+    (torch.nn.functional.softplus's backward); dg/dA_log = g; the per-head
+    parameters' gradients sum over every leading axis.
+    """
+    A_log, a, b, dt_bias, dg, dbeta = (np.asarray(t, np.float64)
+                                       for t in (A_log, a, b, dt_bias, dg, dbeta))
+    bx = sp_beta * (a + dt_bias)
+    with np.errstate(over="ignore"):
+        dsp = np.where(bx > threshold, 1.0, 1.0 / (1.0 + np.exp(-np.minimum(bx, threshold))))
+    g, beta = gating(A_log, a, b, dt_bias, sp_beta, threshold)
+    da = dg * -np.exp(A_log) * dsp
+    db = dbeta * beta * (1.0 - beta)
+    lead = tuple(range(a.ndim - 1))
+    return (dg * g).sum(axis=lead), da, db, da.sum(axis=lead)
 
 
 def causal_conv1d(x, weight, bias=None, seq_idx=None, initial_states=None, silu=False):

@@ -33,6 +33,7 @@ def test_header_declares_expected_entry_points():
                                      "gdn_last_error", "gdn_recurrent_fwd"]
     assert _declared(("gdn_layer.h",)) == [
         "gdn_causal_conv1d_fwd", "gdn_causal_conv1d_update", "gdn_chunk_fwd_gating",
+        "gdn_gating_bwd", "gdn_gating_bwd_workspace_bytes",
         "gdn_gating_fwd", "gdn_l2norm_fwd", "gdn_recurrent_fwd_gating",
         "gdn_recurrent_fwd_indexed", "gdn_recurrent_fwd_spec", "gdn_rmsnorm_gated_fwd"]
 
@@ -219,6 +220,28 @@ def _recs(lib, **kw):
                                       p["slots"], 0.1, 0, None)
 
 
+def _gbwd(lib, **kw):
+    """gdn_gating_bwd with fake (never dereferenced) pointers; rows 8, H 4."""
+    p = dict(A=1 << 20, a=2 << 20, b=3 << 20, dtb=4 << 20, dg=5 << 20, dbeta=6 << 20,
+             dA=7 << 20, da=8 << 20, db=9 << 20, ddt=10 << 20, rows=8, H=4, adt=1, bdt=1,
+             pdt=0, spb=1.0, spt=20.0, ws=11 << 20, wsb=1 << 16)
+    p.update(kw)
+    return lib.gdn_gating_bwd(p["A"], p["a"], p["b"], p["dtb"], p["dg"], p["dbeta"], p["dA"],
+                              p["da"], p["db"], p["ddt"], p["rows"], p["H"], p["adt"],
+                              p["bdt"], p["pdt"], p["spb"], p["spt"], p["ws"], p["wsb"], None)
+
+
+def test_gating_bwd_workspace_bytes(lib):
+    # one (ddt_bias, dA_log) fp32 pair per head and block of 64 rows; at most
+    # 1024 blocks (longer inputs take more rows per block)
+    assert lib.gdn_gating_bwd_workspace_bytes(0, 32) == 0
+    assert lib.gdn_gating_bwd_workspace_bytes(1, 32) == 32 * 8
+    assert lib.gdn_gating_bwd_workspace_bytes(8192, 32) == 128 * 32 * 8
+    assert lib.gdn_gating_bwd_workspace_bytes(1 << 20, 32) == 1024 * 32 * 8
+    assert lib.gdn_gating_bwd_workspace_bytes((1 << 20) + 1, 4) <= 1025 * 4 * 8
+    assert lib.gdn_gating_bwd_workspace_bytes(-1, 4) == 0
+
+
 @pytest.mark.parametrize("call,code,msg", [
     (lambda l: _recs(l, stride=0), -2, "index_stride must be > 0"),
     (lambda l: _recs(l, T=5), -2, "exceeds index_stride"),
@@ -234,6 +257,15 @@ def _recs(lib, **kw):
                                 1, 1, 0, 0.0, 20.0, None), -2, "softplus beta"),
     (lambda l: l.gdn_gating_fwd(None, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 8, 4,
                                 1, 1, 0, 1.0, 20.0, None), -1, "non-NULL"),
+    (lambda l: _gbwd(l, H=0), -2, "0 < H <= 256"),
+    (lambda l: _gbwd(l, H=257), -2, "0 < H <= 256"),
+    (lambda l: _gbwd(l, adt=5), -2, "dtype"),
+    (lambda l: _gbwd(l, spb=0.0), -2, "softplus beta"),
+    (lambda l: _gbwd(l, dg=None), -1, "non-NULL"),
+    (lambda l: _gbwd(l, db=None), -1, "go together"),
+    (lambda l: _gbwd(l, b=None), -1, "need b"),
+    (lambda l: _gbwd(l, ws=None), -4, "workspace"),
+    (lambda l: _gbwd(l, wsb=8), -4, "workspace"),
     (lambda l: l.gdn_l2norm_fwd(1 << 20, 2 << 20, 8, 96, 1e-6, 1, None), -2, "64, 128 or 256"),
     (lambda l: l.gdn_l2norm_fwd(None, 2 << 20, 8, 128, 1e-6, 1, None), -1, "non-NULL"),
     (lambda l: l.gdn_rmsnorm_gated_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 8, 100, 1e-6, 1, 1,
@@ -268,6 +300,7 @@ def test_layer_empty_problems_launch_nothing(lib):
     assert lib.gdn_gating_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20, 6 << 20, 0, 4,
                               1, 1, 0, 1.0, 20.0, None) == 0
     assert lib.gdn_l2norm_fwd(1 << 20, 2 << 20, 0, 128, 1e-6, 1, None) == 0
+    assert _gbwd(lib, rows=0, dA=None, ddt=None, ws=None, wsb=0) == 0
     assert lib.gdn_rmsnorm_gated_fwd(1 << 20, 2 << 20, 3 << 20, 4 << 20, 0, 128, 1e-6, 1, 1,
                                      None) == 0
     assert _conv(lib, B=0) == 0

@@ -52,6 +52,65 @@ def test_gating_softplus_parameters():
     assert g[0, 0] == -21.0
 
 
+def _gating_grad_inputs(seed, shape=(3, 5, 8)):
+    rng = RNG(seed)
+    H = shape[-1]
+    a = rng.standard_normal(shape) * 4
+    a.flat[:3] = [25.0, -30.0, 0.0]              # threshold branch and tails
+    return (np.log(rng.uniform(0.5, 16, H)), a, rng.standard_normal(shape) * 3,
+            rng.standard_normal(H), rng.standard_normal(shape), rng.standard_normal(shape))
+
+
+@pytest.mark.parametrize("spb,spt", [(1.0, 20.0), (2.0, 5.0)])
+def test_gating_bwd_matches_torch_autograd(spb, spt):
+    """gating_bwd against torch's own autograd of the layer's expression (float64, CPU)."""
+    A_log, a, b, dt, dg, dbeta = _gating_grad_inputs(3)
+    ts = [torch.tensor(x, requires_grad=True) for x in (A_log, a, b, dt)]
+    g = -torch.exp(ts[0]) * F.softplus(ts[1] + ts[3], beta=spb, threshold=spt)
+    beta = torch.sigmoid(ts[2])
+    ((g * torch.tensor(dg)).sum() + (beta * torch.tensor(dbeta)).sum()).backward()
+    got = LR.gating_bwd(A_log, a, b, dt, dg, dbeta, spb, spt)
+    for x, t in zip(got, ts):
+        np.testing.assert_allclose(x, t.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+
+def test_gating_bwd_finite_differences():
+    """gating_bwd against central differences of gating itself (away from the threshold)."""
+    A_log, a, b, dt, dg, dbeta = _gating_grad_inputs(4, shape=(4, 6))
+    a.flat[:3] = [2.0, -3.0, 0.5]
+    got = LR.gating_bwd(A_log, a, b, dt, dg, dbeta)
+
+    def loss(A_, a_, b_, d_):
+        g, beta = LR.gating(A_, a_, b_, d_)
+        return (g * dg).sum() + (beta * dbeta).sum()
+
+    args = [A_log, a, b, dt]
+    eps = 1e-6
+    for which, grad in zip(range(4), got):
+        fd = np.zeros_like(args[which])
+        for idx in np.ndindex(args[which].shape):
+            hi = [x.copy() for x in args]
+            lo = [x.copy() for x in args]
+            hi[which][idx] += eps
+            lo[which][idx] -= eps
+            fd[idx] = (loss(*hi) - loss(*lo)) / (2 * eps)
+        np.testing.assert_allclose(grad, fd, rtol=1e-6, atol=1e-8)
+
+
+def test_gating_bwd_mutations_caught():
+    """A softplus derivative at the wrong beta, or a dropped exp(A_log), fails the check."""
+    A_log, a, b, dt, dg, dbeta = _gating_grad_inputs(5)
+    ts = [torch.tensor(x, requires_grad=True) for x in (A_log, a, b, dt)]
+    g = -torch.exp(ts[0]) * F.softplus(ts[1] + ts[3], beta=2.0, threshold=20.0)
+    ((g * torch.tensor(dg)).sum() + (torch.sigmoid(ts[2]) * torch.tensor(dbeta)).sum()).backward()
+    good = LR.gating_bwd(A_log, a, b, dt, dg, dbeta, 2.0, 20.0)
+    np.testing.assert_allclose(good[1], ts[1].grad.numpy(), rtol=1e-12)
+    wrong_scale = LR.gating_bwd(A_log, a, b, dt, dg, dbeta, 1.0, 20.0)[1]
+    assert not np.allclose(wrong_scale, ts[1].grad.numpy(), rtol=1e-6)
+    no_exp = LR.gating_bwd(np.zeros_like(A_log), a, b, dt, dg, dbeta, 2.0, 20.0)[1]
+    assert not np.allclose(no_exp, ts[1].grad.numpy(), rtol=1e-6)
+
+
 # ---------------------------------------------------------- causal conv ----
 def _conv_inputs(B=2, D=6, T=11, W=4, seed=0):
     rng = RNG(seed)
