@@ -113,6 +113,45 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
           rs, ((rg + ROWG * i) * COLG + cg) * 16, 0, kNonTemporal));
   };
 
+  // Shared slots, checked on the device: the slot value of entry j of table
+  // row m if sequence m reads or writes it, else -1 (continuous batching:
+  // the row's one entry; speculative decoding: the initial entry and the
+  // entries of the tokens it has, none for a padding sequence)
+  const int srow = slot_stride > 0 ? slot_stride : 1;
+  auto touched = [&](int m, int j) -> int {
+    const int x = slots[(size_t)m * srow + j];
+    if (x < 0 || x >= num_slots) return -1;
+    if (slot_stride == 0) return x;
+    int col = 0;
+    if (accepted) {
+      col = accepted[m] - 1;
+      if (col < 0 || col >= slot_stride) return -1;
+    }
+    const int init = slots[(size_t)m * slot_stride + col];
+    if (init < 0 || init >= num_slots) return -1;
+    if (j == col) return x;
+    int len = T;
+    if (cu) {
+      const int a = min(max(cu[m], 0), total_tokens);
+      len = min(max(cu[m + 1], a), total_tokens) - a;
+    }
+    return j < len ? x : -1;
+  };
+  // whether a slot sequence n touches is also touched by another sequence
+  // (the whole workgroup scans the table; same answer in every thread)
+  auto shares_slot = [&](int n) -> bool {
+    const int nseq = ntiles / Hv;
+    bool hit = false;
+    for (int idx = tid; idx < nseq * srow; idx += NT) {
+      const int m = idx / srow;
+      if (m == n) continue;
+      const int x = touched(m, idx % srow);
+      if (x < 0) continue;
+      for (int j = 0; j < srow; ++j) hit |= touched(n, j) == x;
+    }
+    return __syncthreads_or(hit) != 0;
+  };
+
   auto run_tile = [&](f32x4 (&S)[RPT], const GateRaw& gr, int tile) {
     const int slot = slot_of(tile);
     if (slot < 0) return;
@@ -126,6 +165,17 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     } else {
       s = n * T;
       e = s + T;
+    }
+    if (slots && shares_slot(n)) {
+      // a slot two sequences would use: neither advances it (no state is
+      // written, so the pool is never written concurrently) and its output
+      // rows are NaN, so the caller's error shows
+      if (rg == 0) {
+        const u16x4 nan4 = {0x7FC0, 0x7FC0, 0x7FC0, 0x7FC0};
+        for (int t = s; t < e; ++t)
+          *reinterpret_cast<u16x4*>(o + ((size_t)t * Hv + h) * V + 4 * cg) = nan4;
+      }
+      return;
     }
     for (int t = s; t < e; ++t) {
       if (GATE && t == s && wave == NW - 1) {

@@ -537,13 +537,18 @@ def _recurrent_indexed(q, k, v, g, beta, scale, pool, output_final_state, cu_seq
 
 
 def _check_distinct_slots(idx: torch.Tensor, num_slots: int, name: str) -> None:
-    """Reject a host-resident slot table that gives two sequences the same slot
-    (their state updates would race); device tables are the caller's contract."""
+    """Reject a host-resident slot table that gives two sequences (rows) the
+    same slot, before anything is launched.  A device-resident table is
+    checked by the kernel itself: every sequence involved leaves its slots
+    untouched and gets NaN output rows."""
     if idx.device.type != "cpu":
         return
-    valid = idx[(idx >= 0) & (idx < num_slots)]
-    if valid.numel() != torch.unique(valid).numel():
-        raise ValueError(f"{name}: ssm_state_indices uses a slot more than once.")
+    if idx.numel() == 0:
+        return
+    rows = idx.reshape(idx.shape[0], -1) if idx.dim() else idx.reshape(1, 1)
+    seen = torch.cat([torch.unique(r[(r >= 0) & (r < num_slots)]) for r in rows])
+    if seen.numel() != torch.unique(seen).numel():
+        raise ValueError(f"{name}: ssm_state_indices gives two sequences the same slot.")
 
 
 def _recurrent_spec(q, k, v, g, beta, scale, pool, cu_seqlens, use_qk_l2norm_in_kernel,

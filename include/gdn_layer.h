@@ -137,6 +137,10 @@ int gdn_rmsnorm_gated_fwd(const void* x, const void* z, const void* weight, void
  * slot state_indices[n] of h0 / ht, which are [num_slots, Hv, K, V].  A
  * slot outside [0, num_slots) marks a padding sequence: its state is not
  * touched and its output rows are not written.  ht may equal h0 (in place).
+ * Sequences must not share a slot; the kernel checks this on the device:
+ * every sequence whose slot another sequence also names leaves that slot
+ * untouched and gets NaN output rows (so the pool is never written by two
+ * workgroups at once, and the caller's mistake shows in o).
  */
 int gdn_recurrent_fwd_indexed(const void* q, const void* k, const void* v,
                               const float* g, const float* beta,
@@ -163,7 +167,10 @@ int gdn_recurrent_fwd_indexed(const void* q, const void* k, const void* v,
  *   pool                 [num_slots, Hv, K, V] fp32, read and written in place.
  * Without cu_seqlens every sequence has T tokens and T <= index_stride is
  * required; with cu_seqlens, tokens past index_stride advance the state
- * without writing it.  Sequences must not share slots.
+ * without writing it.  Sequences must not share slots (a row may repeat its
+ * own): checked on the device as for gdn_recurrent_fwd_indexed, over the
+ * entries each sequence reads or writes (its initial entry and those of its
+ * tokens) -- every sequence involved writes no state and gets NaN outputs.
  */
 int gdn_recurrent_fwd_spec(const void* q, const void* k, const void* v,
                            const float* g, const float* beta, float* pool, void* o,

@@ -99,7 +99,10 @@ def test_host_slot_table_rejects_shared_slots():
     from avelang_amd.gated_delta_rule import _check_distinct_slots
     _check_distinct_slots(torch.tensor([0, 2, -1, -1, 5], dtype=torch.int32), 6, "op")
     _check_distinct_slots(torch.tensor([[0, 1], [2, 9]], dtype=torch.int32), 6, "op")
-    with pytest.raises(ValueError, match="more than once"):
+    # a row may repeat its own slot (speculative decoding: several tokens' states into one)
+    _check_distinct_slots(torch.tensor([[1, 1], [2, 3]], dtype=torch.int32), 6, "op")
+    _check_distinct_slots(torch.zeros((0,), dtype=torch.int32), 6, "op")
+    with pytest.raises(ValueError, match="two sequences the same slot"):
         _check_distinct_slots(torch.tensor([0, 2, 2], dtype=torch.int32), 6, "op")
-    with pytest.raises(ValueError, match="more than once"):
+    with pytest.raises(ValueError, match="two sequences the same slot"):
         _check_distinct_slots(torch.tensor([[0, 1], [1, 3]], dtype=torch.int32), 6, "op")
