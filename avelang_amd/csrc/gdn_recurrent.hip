@@ -36,6 +36,10 @@ constexpr int kNonTemporal = 2;
 #endif
 // workgroups of the persistent decode grid
 constexpr int kDecodeGrid = GDN_DECODE_GRID;
+// pool slots and sequences up to which the shared-slot check of a slot
+// table runs once per workgroup in LDS (beyond: at every tile)
+constexpr int kSlotOwn = 4096;
+constexpr int kSlotSeq = 4096;
 
 // Persistent form: a workgroup walks tiles blockIdx.x, +G, +2G, ... and
 // loads the next tile's state while it advances the current one, so the
@@ -65,6 +69,8 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
   __shared__ float kq_s[2][K];
   __shared__ float red[NW][COLG][NRED + 1];
   __shared__ float gsh[2];   // GATE: g, beta of a tile's first token
+  __shared__ int sown[kSlotOwn];              // slot tables: lowest sequence per slot
+  __shared__ unsigned sflag[kSlotSeq / 32];   // and a bit per sequence sharing one
 
   const int tid = threadIdx.x;
   const int cg = tid % COLG;
@@ -137,15 +143,44 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(
     }
     return j < len ? x : -1;
   };
-  // whether a slot sequence n touches is also touched by another sequence
-  // (the whole workgroup scans the table; same answer in every thread)
-  auto shares_slot = [&](int n) -> bool {
-    const int nseq = ntiles / Hv;
-    bool hit = false;
-    for (int idx = tid; idx < nseq * srow; idx += NT) {
+  // Which sequences share a slot does not depend on the tile, so with at
+  // most kSlotOwn slots and kSlotSeq sequences a workgroup finds them all
+  // once, before its first tile: the lowest sequence touching each slot
+  // (LDS atomic min), then every entry whose slot has another lowest
+  // sequence marks both sequences (a bit per sequence).  A tile then reads
+  // its sequence's bit.  Larger tables are scanned at every tile instead.
+  const int nseq = ntiles / Hv;
+  const int nent = slots ? nseq * srow : 0;
+  const bool own_lds = num_slots <= kSlotOwn && nseq <= kSlotSeq;
+  if (slots && own_lds) {
+    for (int x = tid; x < num_slots; x += NT) sown[x] = 0x7fffffff;
+    for (int w = tid; w < (nseq + 31) / 32; w += NT) sflag[w] = 0u;
+    __syncthreads();
+    for (int idx = tid; idx < nent; idx += NT) {
+      const int x = touched(idx / srow, idx % srow);
+      if (x >= 0) atomicMin(&sown[x], idx / srow);
+    }
+    __syncthreads();
+    for (int idx = tid; idx < nent; idx += NT) {
       const int m = idx / srow;
-      if (m == n) continue;
       const int x = touched(m, idx % srow);
+      if (x < 0) continue;
+      const int first = sown[x];
+      if (first != m) {
+        atomicOr(&sflag[m >> 5], 1u << (m & 31));
+        atomicOr(&sflag[first >> 5], 1u << (first & 31));
+      }
+    }
+    __syncthreads();
+  }
+  // whether a slot sequence n touches is also touched by another sequence
+  // (same answer in every thread of the workgroup)
+  auto shares_slot = [&](int n) -> bool {
+    if (own_lds) return (sflag[n >> 5] >> (n & 31)) & 1u;
+    bool hit = false;
+    for (int idx = tid; idx < nent; idx += NT) {
+      if (idx / srow == n) continue;
+      const int x = touched(idx / srow, idx % srow);
       if (x < 0) continue;
       for (int j = 0; j < srow; ++j) hit |= touched(n, j) == x;
     }

@@ -138,3 +138,23 @@ def test_spec_unused_entries_do_not_count(rocm_device):
     assert (_rows(o, wl, 2) == 7.0).all()
     assert torch.equal(pool, ref_pool)
     assert not torch.equal(pool[5], before[5])                       # row 1's last token
+
+
+def test_indexed_shared_slot_large_pool(rocm_device):
+    """A pool of more than 4096 slots takes the per-tile form of the check (the workgroup
+    scans the table at every tile): the same outcome."""
+    dev = rocm_device
+    N, nslots = 5, 5000
+    wl = W.make(N, 1, 2, 4, 64, 64, seed=76, h0_scale=0.01)
+    pool = 0.01 * torch.randn((nslots, 4, 64, 64), device=dev)
+    before = pool.clone()
+    idx = torch.tensor([4999, 17, 4200, 17, 3], dtype=torch.int32)   # 1 and 3 share 17
+    o = _decode(dev, wl, pool, idx)
+    ref_pool = before.clone()
+    o_ref = _decode(dev, wl, ref_pool, torch.tensor([4999, -1, 4200, -1, 3], dtype=torch.int32))
+    for n in (1, 3):
+        assert torch.isnan(o[n].float()).all(), n
+    for n in (0, 2, 4):
+        assert torch.equal(o[n], o_ref[n]), n
+    assert torch.equal(pool, ref_pool)
+    assert not torch.equal(pool[4999], before[4999])
