@@ -39,7 +39,8 @@ struct ChunkWs {
   u16x8* qtfrag;    // [NC][Hqk][K/16][2][64] fp16 A-operand fragments of Q^T (key-row
                     // tile, token k-block; the l2-normalised q with use_qk_l2norm)
   uint16_t* hs;     // [NC][Hv][V][K] bf16: state at the start of every chunk, transposed
-  uint16_t* dl;     // [B*T][Hv][V]   bf16: d = vnew, the per-token delta
+  uint16_t* dl;     // [NC][Hv][V/8][64][8] bf16: d = vnew, the per-token delta, per
+                    // chunk in column groups of 8 (rows past the sequence end 0)
 };
 
 // Packed T: the 10 lower 16 x 16 blocks of the 64 x 64 matrix, block

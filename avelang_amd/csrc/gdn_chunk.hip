@@ -532,8 +532,8 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
     p.ptfrag = take(nch * 4 * 2 * 64 * 16);
     p.hs = take(nch * K * V * 2);
     p.dse = take(nch * K * V * 2);
-    p.dl = take((size_t)total * Hv * V * 2);
-    p.dd = take((size_t)total * Hv * V * 2);
+    p.dl = take(nch * 64 * V * 2);
+    p.dd = take(nch * 64 * V * 2);
     p.qtfrag = take((size_t)p.ncmax * Hqk * (K / 16) * 2 * 64 * 16);
   }
   p.total = at;

@@ -35,7 +35,8 @@ namespace gdn {
 struct BwdWs {
   ChunkWs f;              // forward workspace (gate, fragments, T, hs, dl, ...)
   uint16_t* dse;          // [NC][Hv][V][K] bf16: dL/d(end state) of every chunk, transposed
-  uint16_t* dd;           // [B*T][Hv][V]   bf16: dL/dd
+  uint16_t* dd;           // [NC][Hv][V/8][64][8] bf16: dL/dd, per chunk in column
+                          // groups of 8 (rows past the sequence end 0)
 };
 
 // --------------------------------------------------- gradient kernel ----
@@ -291,6 +292,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const int ss_v = (tid % NPOS) / 4, ss_k = 8 * (tid % 4);
     const int sp_vs = (ss_v * K + ss_k) * 2;
     const int sp_vt = (sp_r * Hv * V + sp_c8) * 2;
+    const int sp_dl = ((sp_c8 >> 3) * 64 + sp_r) * 16;
     const int h = hq * Gn + gi_t;
     const size_t ch = (size_t)ci * Hv + h;
     const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
@@ -300,9 +302,9 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const __amdgpu_buffer_rsrc_t rT = __builtin_amdgcn_make_buffer_rsrc(
         ws.f.tmat + ch * kTPacked, 0, live ? kTPacked * 4 : 0, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdd = __builtin_amdgcn_make_buffer_rsrc(
-        ws.dd + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+        ws.dd + ch * 64 * V, 0, live ? 64 * V * 2 : 0, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
-        ws.f.dl + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+        ws.f.dl + ch * 64 * V, 0, live ? 64 * V * 2 : 0, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -317,7 +319,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
           pre[i][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rE, sp_vs, so, 0));
         } else {
           const int so = 32 * (sl - NSS) * Hv * V * 2;
-          pre[i][0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_vt, so, 0));
+          pre[i][0] = __builtin_bit_cast(
+              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_dl, 32 * (sl - NSS) * 16, 0));
           pre[i][1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, sp_vt, so, 0));
         }
       }
@@ -330,9 +333,9 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     }
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
-      const int idx = tid + NTH * i, r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
-      dv8[i] = __builtin_bit_cast(
-          u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, (r * Hv * V + c8) * 2, 0, 0));
+      // 16-byte chunk idx: token row idx % 64 of column group idx / 64
+      const int idx = tid + NTH * i;
+      dv8[i] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdd, idx * 16, 0, 0));
     }
     if (tid < 64) {
       gsv = ws.f.gate[ch * 64 + tid];
@@ -370,6 +373,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const int ss_v = (tid % NPOS) / 4, ss_k = 8 * (tid % 4);
     const int sp_vs = (ss_v * K + ss_k) * 2;             // byte offset in a state slice
     const int sp_vt = (sp_r * Hv * V + sp_c8) * 2;       // byte offset in a token slice
+    const int sp_dl = ((sp_c8 >> 3) * 64 + sp_r) * 16;   // the same in the chunk's d block
     const int h = hq * Gn + gi;
     const size_t ch = (size_t)ci * Hv + h;
     const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
@@ -377,7 +381,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     const __amdgpu_buffer_rsrc_t rE = __builtin_amdgcn_make_buffer_rsrc(
         ws.dse + ch * K * V, 0, K * V * 2, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rdl = __builtin_amdgcn_make_buffer_rsrc(
-        ws.f.dl + ((size_t)t0 * Hv + h) * V, 0, vbytes, kBufferFlags);
+        ws.f.dl + ch * 64 * V, 0, 64 * V * 2, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(v + ((size_t)t0 * Hv + h) * V), 0, vbytes, kBufferFlags);
 
@@ -396,7 +400,8 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
         buf[1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rE, sp_vs, so, 0));
       } else {
         const int so = 32 * (sl - NSS) * Hv * V * 2;
-        buf[0] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_vt, so, 0));
+        buf[0] = __builtin_bit_cast(
+            u16x8, __builtin_amdgcn_raw_buffer_load_b128(rdl, sp_dl, 32 * (sl - NSS) * 16, 0));
         buf[1] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, sp_vt, so, 0));
       }
     };
@@ -441,7 +446,7 @@ __global__ __launch_bounds__(kGradThreads) void chunk_grad_kernel(
     }
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
-      const int idx = tid + NTH * i, r = idx / (V / 8), c8 = 8 * (idx % (V / 8));
+      const int idx = tid + NTH * i, r = idx % 64, c8 = 8 * (idx / 64);
       *reinterpret_cast<u16x8*>(&dds[r][c8]) = dv8[i];
     }
     if (tid < 64) {

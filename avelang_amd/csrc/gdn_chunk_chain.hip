@@ -404,11 +404,13 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
                                                0, 0);
       // deltas: lane t gathers token row t (its 16 columns) from the vnew
       // fragments in LDS -- element (t % 8) of fragment lane 16 ((t / 8) % 4)
-      // + n of k-block t / 32 -- and writes it with two 16-byte stores
+      // + n of k-block t / 32 -- and stores it into the chunk's d block
+      // ([V / 8 column groups][64 tokens][8], each store one contiguous 1 KiB;
+      // rows past the sequence end 0)
       const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
-          ws.dl + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+          ws.dl + (ci * Hv + h) * 64 * V, 0, live ? 64 * V * 2 : 0, kBufferFlags);
       u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
-      if (live) {
+      if (live && lane < L) {
         const uint16_t* src =
             reinterpret_cast<const uint16_t*>(&Vx[b3][sl][lane >> 5][16 * ((lane >> 3) & 3)]) +
             (lane & 7);
@@ -420,9 +422,10 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
         d0 = h2bf8(d0);
         d1 = h2bf8(d1);
       }
-      const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr, drow, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), dr, drow + 16, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr,
+                                             ((2 * vt) * 64 + lane) * 16, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), dr,
+                                             ((2 * vt + 1) * 64 + lane) * 16, 0, 0);
       }
     };
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));

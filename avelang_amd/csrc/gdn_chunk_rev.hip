@@ -5,7 +5,8 @@
 //     dd = P^T dO + e^(G_L - G) (K dS'),   Z = Tb^T dd,
 //     dS = e^G_L dS' - K^T (e^G Z) + Q^T (c' e^G dO)
 // and dS becomes the previous chunk's dS'.  Stored for the gradient kernel:
-// dS' of every chunk (bf16, transposed) and dd (bf16, token-major); dh0.
+// dS' of every chunk (bf16, transposed) and dd (bf16, per chunk in column
+// groups of 8); dh0.
 //
 // The layout of the forward chain (gdn_chunk_chain.hip), with two helper
 // waves in place of its output wave:
@@ -24,8 +25,10 @@
 //
 //   waves 2 and 3, the helper waves, form the next step's gate factors and
 //   P^T dO (wave 2) and Q^T (c' e^G dO) (wave 3) from the prep's P^T and
-//   Q^T fragments and dO, write them into LDS, and store the previous
-//   step's dS' and dd (wave 2).
+//   Q^T fragments and dO (16-byte row loads, transposed through LDS), and
+//   write them into LDS.
+//
+//   wave 4, the save wave, stores the previous step's dS' and dd.
 //
 // Step j works on chunk nc - 1 - j of the sequence.
 #include <type_traits>
@@ -35,7 +38,7 @@
 namespace gdn {
 
 template <int K>
-__global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
+__global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
     const uint16_t* __restrict__ dO, const float* dht,
     float* dh0, const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
     float scale, ChunkWs ws, uint16_t* __restrict__ dse, uint16_t* __restrict__ ddo) {
@@ -56,6 +59,9 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
   // as B fragments
   __shared__ __attribute__((aligned(16))) u16x8 Sx[3][KB][64];
   __shared__ __attribute__((aligned(16))) u16x8 Vx[3][2][64];
+  // each helper wave's dO tile (bf16 [token][16 columns]), written from its
+  // 16-byte row loads and read back transposed as B fragments
+  __shared__ __attribute__((aligned(16))) uint16_t Dh[2][64][16];
 
   const int NVT = V / 16;
   int bid = blockIdx.x;
@@ -240,10 +246,10 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // step j+1's
       barrier();
     }
-  } else {
+  } else if (w <= 3) {
     // ---------------------------------------------------- helper waves ----
-    // Wave 2 forms step j+1's gate factors and P^T dO into LDS and stores
-    // step j-1's dS' and dd; wave 3 forms step j+1's Q^T (c' e^G dO).  Each
+    // Wave 2 forms step j+1's gate factors and P^T dO into LDS; wave 3 forms
+    // step j+1's Q^T (c' e^G dO).  Each
     // uses the register set it loaded two steps before and then loads step
     // j+3's operands into it.  Every step issues the same loads and stores,
     // so each wait names an exact count.
@@ -251,13 +257,15 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
     // two roles' loads blurs the compiler's wait counts
     auto helper = [&](auto qwc) {
       constexpr bool qwave = decltype(qwc)::value;
-      constexpr int kStep = qwave ? 2 * ST + 16 + 1 : 6 + 16 + 1 + KB + 2;
+      constexpr int kStep = qwave ? 2 * ST + 2 + 1 : 6 + 2 + 1;
+      typedef unsigned int u32x4l __attribute__((ext_vector_type(4)));
       struct Regs {
         u16x8 pt[6];        // P^T fragments (rho rows, bf16) by tb_slot (wave 2)
         u16x8 qt[ST][2];    // Q^T fragments (rho key rows, fp16) by token k-block (wave 3)
-        u16x8 dof[2];       // dO[32 kb + 8 grp + i][16 vt + r16] (B operand)
+        u32x4l dor[2];      // dO rows 32 x + lane / 2, columns 8 (lane % 2) .. + 7
         float G;            // G of token `lane`
       };
+      uint16_t (*dh)[16] = Dh[w - 2];
       Regs rA, rB;
       auto load = [&](Regs& r, int j) {
         const int jc = nc - 1 - j;
@@ -286,17 +294,17 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
             }
           }
         }
+        // the chunk's dO tile as 16-byte row pieces (two per token row, rows
+        // past the sequence end read as 0)
         const int rowb = Hv * V * 2;
         const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V + 16 * vt), 0,
             (L - 1) * rowb + 32, kBufferFlags);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            r.dof[kb][i] = __builtin_amdgcn_raw_buffer_load_b16(
-                rd, (32 * kb + 8 * grp + i) * rowb + 2 * r16, 0, 0);
-        }
+        for (int x = 0; x < 2; ++x)
+          r.dor[x] = __builtin_bit_cast(
+              u32x4l, __builtin_amdgcn_raw_buffer_load_b128(
+                          rd, (32 * x + (lane >> 1)) * rowb + 16 * (lane & 1), 0, 0));
         const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
             ws.gate + ((size_t)ci * Hv + h) * 64, 0, 256, kBufferFlags);
         r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
@@ -306,6 +314,14 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
       auto publish = [&](const Regs& r, int j) {
         const int buf = j % 3;
         const float eg = __expf(r.G);
+        // dO B fragments: element i of lane (r16, grp), k-block kb is
+        // dO[32 kb + 8 grp + i][16 vt + r16], through this wave's LDS tile
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+          *reinterpret_cast<u32x4l*>(&dh[32 * x + (lane >> 1)][8 * (lane & 1)]) = r.dor[x];
+        u16x8 dof[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) dof[kb] = lds_colfrag(&dh[0][0], 16, 32 * kb, 0, lane);
         if constexpr (qwave) {
           // c' e^G dO for this lane's k-slots (tokens 32 kb + 8 grp + i), fp16
           u16x8 oh[2];
@@ -317,8 +333,8 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
               const int src = 4 * (32 * kb + 8 * grp + i);
               const float e0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(eg)));
               const float e1 = __int_as_float(__builtin_amdgcn_ds_bpermute(src + 16, __float_as_int(eg)));
-              x0[i] = scale * e0 * bf2f(r.dof[kb][i]);
-              x1[i] = scale * e1 * bf2f(r.dof[kb][4 + i]);
+              x0[i] = scale * e0 * bf2f(dof[kb][i]);
+              x1[i] = scale * e1 * bf2f(dof[kb][4 + i]);
             }
             oh[kb] = cat8(f2h4(x0), f2h4(x1));
           }
@@ -338,64 +354,17 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
           if (lane == L - 1) Egl[buf] = eg;
 #pragma unroll
           for (int ti = 0; ti < 4; ++ti) {
-            f32x4 pd = mfma16(r.pt[tb_slot(ti, 1)], r.dof[1], zero4());
-            if (ti < 2) pd = mfma16(r.pt[tb_slot(ti, 0)], r.dof[0], pd);
+            f32x4 pd = mfma16(r.pt[tb_slot(ti, 1)], dof[1], zero4());
+            if (ti < 2) pd = mfma16(r.pt[tb_slot(ti, 0)], dof[0], pd);
             Pst[buf][ti][lane] = pd;
           }
         }
-      };
-      typedef unsigned int u32x4l __attribute__((ext_vector_type(4)));
-      // step j's dS' (dse[chunk][v-head] = dS'^T, [V][K], bf16) and dd
-      // (token-major), wave 2; live = false (no step yet) stores to empty
-      // resources
-      auto save = [&](int j, bool live) {
-        if constexpr (qwave) return;
-        const int jc = nc - 1 - j;
-        const int t0 = s + jc * kChunk, L = live ? min(kChunk, e - t0) : 0;
-        const int b3 = j % 3;
-        const size_t ci = live ? (size_t)(c_begin + jc) : 0;
-        // store i, lane l: row 16 vt + rpi i + l / cpr, columns 8 (l % cpr)
-        // .. + 7, i.e. rpi whole rows per store (fragment lane r16 + 16 grp
-        // of k-block b holds row r16, columns 32 b + 8 grp .. + 7)
-        constexpr int cpr = K / 8, rpi = 64 / cpr;
-        const int c8 = lane % cpr;
-        u16x8 sh[KB];
-        if (live) {
-#pragma unroll
-          for (int i = 0; i < KB; ++i) sh[i] = Sx[b3][c8 >> 2][(rpi * i + lane / cpr) + 16 * (c8 & 3)];
-        }
-        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
-            dse + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
-#pragma unroll
-        for (int i = 0; i < KB; ++i)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, sh[i]), hr,
-                                                 ((16 * vt + rpi * i + lane / cpr) * K + 8 * c8) * 2,
-                                                 0, 0);
-        // lane t gathers token row t of dd from the fragments in LDS (element
-        // t % 8 of fragment lane 16 ((t / 8) % 4) + n of k-block t / 32)
-        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
-            ddo + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-        u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
-        if (live) {
-          const uint16_t* src =
-              reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
-              (lane & 7);
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            d0[c] = src[8 * c];
-            d1[c] = src[8 * (c + 8)];
-          }
-        }
-        const int drow = ((lane * Hv + h) * V + 16 * vt) * 2;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d0), dr, drow, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d1), dr, drow + 16, 0, 0);
       };
       if (nc > 0) {
         load(rA, 0);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         publish(rA, 0);
         load(rB, min(1, nc - 1));
-        save(0, false);                  // the stores a step issues, dropped
         load(rA, min(2, nc - 1));
       }
       __syncthreads();
@@ -403,7 +372,6 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
       auto hstep = [&](int j, Regs& r) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(kStep));   // step j+1's operands
         if (j + 1 < nc) publish(r, j + 1);
-        save(j - 1, j >= 1);
         load(r, min(j + 3, nc - 1));
         __syncthreads();
       };
@@ -413,13 +381,68 @@ __global__ __launch_bounds__(256) void chunk_rev_sw_kernel(
         hstep(j + 1, rA);
       }
       if (j < nc) hstep(j, rB);
-      if (nc > 0) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        save(nc - 1, true);
-      }
     };
     if (w == 3) helper(std::true_type{});
     else helper(std::false_type{});
+  } else {
+    // ------------------------------------------------------- save wave ----
+    // Step j-1's dS' and dd during step j (their LDS buffers live until
+    // step j+2 overwrites them): the stores have a wave of their own, off the
+    // helper waves, which set the step.
+    typedef unsigned int u32x4l __attribute__((ext_vector_type(4)));
+    // step j's dS' (dse[chunk][v-head] = dS'^T, [V][K], bf16) and dd
+    // (token-major)
+    auto save = [&](int j, bool live) {
+      const int jc = nc - 1 - j;
+      const int t0 = s + jc * kChunk, L = live ? min(kChunk, e - t0) : 0;
+      const int b3 = j % 3;
+      const size_t ci = live ? (size_t)(c_begin + jc) : 0;
+      // store i, lane l: row 16 vt + rpi i + l / cpr, columns 8 (l % cpr)
+      // .. + 7, i.e. rpi whole rows per store (fragment lane r16 + 16 grp
+      // of k-block b holds row r16, columns 32 b + 8 grp .. + 7)
+      constexpr int cpr = K / 8, rpi = 64 / cpr;
+      const int c8 = lane % cpr;
+      u16x8 sh[KB];
+      if (live) {
+#pragma unroll
+        for (int i = 0; i < KB; ++i) sh[i] = Sx[b3][c8 >> 2][(rpi * i + lane / cpr) + 16 * (c8 & 3)];
+      }
+      const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+          dse + (ci * Hv + h) * V * K, 0, live ? V * K * 2 : 0, kBufferFlags);
+#pragma unroll
+      for (int i = 0; i < KB; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, sh[i]), hr,
+                                               ((16 * vt + rpi * i + lane / cpr) * K + 8 * c8) * 2,
+                                               0, 0);
+      // lane t gathers token row t of dd from the fragments in LDS (element
+      // t % 8 of fragment lane 16 ((t / 8) % 4) + n of k-block t / 32) and
+      // stores it into the chunk's dd block ([V / 8 column groups][64 tokens]
+      // [8], so that each store is one contiguous 1 KiB; rows past the
+      // sequence end 0)
+      const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+          ddo + (ci * Hv + h) * 64 * V, 0, live ? 64 * V * 2 : 0, kBufferFlags);
+      u16x8 d0 = {0, 0, 0, 0, 0, 0, 0, 0}, d1 = d0;
+      if (live && lane < L) {
+        const uint16_t* src =
+            reinterpret_cast<const uint16_t*>(&Vx[b3][lane >> 5][16 * ((lane >> 3) & 3)]) +
+            (lane & 7);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          d0[c] = src[8 * c];
+          d1[c] = src[8 * (c + 8)];
+        }
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d0), dr,
+                                             ((2 * vt) * 64 + lane) * 16, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d1), dr,
+                                             ((2 * vt + 1) * 64 + lane) * 16, 0, 0);
+    };
+    __syncthreads();
+    for (int j = 0; j < nc; ++j) {
+      if (j >= 1) save(j - 1, true);
+      __syncthreads();
+    }
+    if (nc > 0) save(nc - 1, true);
   }
 }
 
@@ -427,7 +450,7 @@ template <int K>
 void launch_rev_sw(const uint16_t* dO, const float* dht, float* dh0, const int32_t* cu, int N,
                    int T, int total, int Hqk, int Hv, int V, float scale, const ChunkWs& ws,
                    uint16_t* dse, uint16_t* dd, hipStream_t st) {
-  hipLaunchKernelGGL((chunk_rev_sw_kernel<K>), dim3(N * Hv * (V / 16)), dim3(256), 0, st, dO,
+  hipLaunchKernelGGL((chunk_rev_sw_kernel<K>), dim3(N * Hv * (V / 16)), dim3(320), 0, st, dO,
                      dht, dh0, cu, N, T, total, Hqk, Hv, V, scale, ws, dse, dd);
 }
 
