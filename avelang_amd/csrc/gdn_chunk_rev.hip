@@ -8,7 +8,7 @@
 // dS' of every chunk (bf16, transposed) and dd (bf16, per chunk in column
 // groups of 8); dh0.
 //
-// The layout of the forward chain (gdn_chunk_chain.hip), with two helper
+// The layout of the forward chain (gdn_chunk_chain.hip), with three helper
 // waves in place of its output wave:
 //
 //   wave 0, the state wave, holds every key row of the tile's dS' in VGPRs
@@ -21,14 +21,14 @@
 //
 //   wave 1, the stage wave, copies the chunk's fp16 K block and Tb^T
 //   fragments two steps ahead straight into LDS (buffer_load ... lds), both
-//   contiguous as the prep kernel laid them out.
+//   contiguous as the prep kernel laid them out, and the dO tile three steps
+//   ahead.
 //
-//   waves 2 and 3, the helper waves, form the next step's gate factors and
-//   P^T dO (wave 2) and Q^T (c' e^G dO) (wave 3) from the prep's P^T and
-//   Q^T fragments and dO (16-byte row loads, transposed through LDS), and
-//   write them into LDS.
-//
-//   wave 4, the save wave, stores the previous step's dS' and dd.
+//   waves 2 to 4, the helper waves, form the next step's gate factors and
+//   P^T dO (wave 2) and Q^T (c' e^G dO) (waves 3 and 4, half the state
+//   tiles each) from the prep's P^T and Q^T fragments and dO (the stage
+//   wave's tile, read transposed), and write them into LDS; wave 4 also
+//   stores the previous step's dS' and dd.
 //
 // Step j works on chunk nc - 1 - j of the sequence.
 #include <type_traits>
@@ -59,9 +59,10 @@ __global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
   // as B fragments
   __shared__ __attribute__((aligned(16))) u16x8 Sx[3][KB][64];
   __shared__ __attribute__((aligned(16))) u16x8 Vx[3][2][64];
-  // each helper wave's dO tile (bf16 [token][16 columns]), written from its
-  // 16-byte row loads and read back transposed as B fragments
-  __shared__ __attribute__((aligned(16))) uint16_t Dh[2][64][16];
+  // the dO tile of step j (bf16 [token][16 columns]) in slot j % 4, copied
+  // by the stage wave three steps ahead and read transposed by the helpers
+  __shared__ __attribute__((aligned(16))) uint16_t Dst[4][64][16];
+  __shared__ __attribute__((aligned(16))) float Eq[2][64];   // Q waves 3, 4: c' e^G by token
 
   const int NVT = V / 16;
   int bid = blockIdx.x;
@@ -101,7 +102,8 @@ __global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
 #pragma unroll
       for (int t = 0; t < ST; ++t) S[t] = zero4();
     }
-    __syncthreads();   // stage buffer 0 and the helper's first tiles are in
+    __syncthreads();   // stage buffer 0 and step 0's dO are in
+    __syncthreads();   // the helpers' step-0 tiles are in
 
     const int m4 = r16 >> 2, q4 = r16 & 3;
     int ka_off[4];
@@ -212,10 +214,28 @@ __global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
     // As in the forward chain: step j + 2's fp16 K block (KLayout, rows
     // past the sequence end zero) and Tb^T fragments (rho rows) straight to
     // LDS during step j, lane l of load i copying bytes 16 (64 i + l) of the
-    // contiguous source; bare barriers, explicit waits.
+    // contiguous source; bare barriers, explicit waits.  With them, step
+    // j + 3's dO tile (the helpers form step j + 1's terms during step j, so
+    // their dO must be in one step earlier than the stage buffers).
     typedef __attribute__((address_space(3))) void* lds_ptr;
-    constexpr int kKT = KL::LOADS + 6;
+    constexpr int kKT = KL::LOADS + 6 + 2;
+    const int rowd = Hv * V * 2;
+    // step jd's dO tile into slot jd % 4 (past the last step: the last
+    // step's again, into a slot no later step reads): load x, lane l copies
+    // half l % 2 of token row 32 x + l / 2 (rows past the sequence end 0)
+    auto issue_do = [&](int jd) {
+      const int jc = nc - 1 - min(jd, nc - 1);
+      const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
+      const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(dO + (size_t)t0 * Hv * V), 0, L * rowd, kBufferFlags);
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rd, (lds_ptr)&Dst[jd % 4][32 * x][0], 16,
+            (32 * x + (lane >> 1)) * rowd + (h * V + 16 * vt) * 2 + 16 * (lane & 1), 0, 0, 0);
+    };
     auto issue_kt = [&](int j, int jb) {
+      issue_do(jb + 1);
       const int ci = c_begin + nc - 1 - j, buf = jb % 3;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
           ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES, 0, KL::BYTES, kBufferFlags);
@@ -236,162 +256,31 @@ __global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
     };
     if (nc > 0) {
+      issue_do(0);
       issue_kt(0, 0);
       issue_kt(min(1, nc - 1), 1);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // step 0's
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // step 0's (and dO of 0, 1)
     }
     barrier();
+    barrier();   // the helpers' step-0 tiles
     for (int j = 0; j < nc; ++j) {
       issue_kt(min(j + 2, nc - 1), j + 2);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // step j+1's
       barrier();
     }
-  } else if (w <= 3) {
-    // ---------------------------------------------------- helper waves ----
-    // Wave 2 forms step j+1's gate factors and P^T dO into LDS; wave 3 forms
-    // step j+1's Q^T (c' e^G dO).  Each
-    // uses the register set it loaded two steps before and then loads step
-    // j+3's operands into it.  Every step issues the same loads and stores,
-    // so each wait names an exact count.
-    // one code path per role (a compile-time flag), so that no join of the
-    // two roles' loads blurs the compiler's wait counts
-    auto helper = [&](auto qwc) {
-      constexpr bool qwave = decltype(qwc)::value;
-      constexpr int kStep = qwave ? 2 * ST + 2 + 1 : 6 + 2 + 1;
-      typedef unsigned int u32x4l __attribute__((ext_vector_type(4)));
-      struct Regs {
-        u16x8 pt[6];        // P^T fragments (rho rows, bf16) by tb_slot (wave 2)
-        u16x8 qt[ST][2];    // Q^T fragments (rho key rows, fp16) by token k-block (wave 3)
-        u32x4l dor[2];      // dO rows 32 x + lane / 2, columns 8 (lane % 2) .. + 7
-        float G;            // G of token `lane`
-      };
-      uint16_t (*dh)[16] = Dh[w - 2];
-      Regs rA, rB;
-      auto load = [&](Regs& r, int j) {
-        const int jc = nc - 1 - j;
-        const int ci = c_begin + jc;
-        const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
-        if constexpr (qwave) {
-          const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-              ws.qtfrag + ((size_t)ci * Hqk + hq) * ST * 128, 0, ST * 128 * 16, kBufferFlags);
-#pragma unroll
-          for (int t = 0; t < ST; ++t) {
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-              r.qt[t][b] = __builtin_bit_cast(
-                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((2 * t + b) * 64 + lane) * 16, 0, 0));
-          }
-        } else {
-          const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-              ws.ptfrag + ((size_t)ci * Hv + h) * 4 * 128, 0, 4 * 128 * 16, kBufferFlags);
-#pragma unroll
-          for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-              if (b == 0 && ti >= 2) continue;
-              r.pt[tb_slot(ti, b)] = __builtin_bit_cast(
-                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, ((2 * ti + b) * 64 + lane) * 16, 0, 0));
-            }
-          }
-        }
-        // the chunk's dO tile as 16-byte row pieces (two per token row, rows
-        // past the sequence end read as 0)
-        const int rowb = Hv * V * 2;
-        const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(dO + ((size_t)t0 * Hv + h) * V + 16 * vt), 0,
-            (L - 1) * rowb + 32, kBufferFlags);
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-          r.dor[x] = __builtin_bit_cast(
-              u32x4l, __builtin_amdgcn_raw_buffer_load_b128(
-                          rd, (32 * x + (lane >> 1)) * rowb + 16 * (lane & 1), 0, 0));
-        const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
-            ws.gate + ((size_t)ci * Hv + h) * 64, 0, 256, kBufferFlags);
-        r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
-      };
-      // step j's gate factors and P^T dO (wave 2) or Q^T (c' e^G dO) (wave 3)
-      // into buffer j % 3
-      auto publish = [&](const Regs& r, int j) {
-        const int buf = j % 3;
-        const float eg = __expf(r.G);
-        // dO B fragments: element i of lane (r16, grp), k-block kb is
-        // dO[32 kb + 8 grp + i][16 vt + r16], through this wave's LDS tile
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-          *reinterpret_cast<u32x4l*>(&dh[32 * x + (lane >> 1)][8 * (lane & 1)]) = r.dor[x];
-        u16x8 dof[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) dof[kb] = lds_colfrag(&dh[0][0], 16, 32 * kb, 0, lane);
-        if constexpr (qwave) {
-          // c' e^G dO for this lane's k-slots (tokens 32 kb + 8 grp + i), fp16
-          u16x8 oh[2];
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            f32x4 x0, x1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int src = 4 * (32 * kb + 8 * grp + i);
-              const float e0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(eg)));
-              const float e1 = __int_as_float(__builtin_amdgcn_ds_bpermute(src + 16, __float_as_int(eg)));
-              x0[i] = scale * e0 * bf2f(dof[kb][i]);
-              x1[i] = scale * e1 * bf2f(dof[kb][4 + i]);
-            }
-            oh[kb] = cat8(f2h4(x0), f2h4(x1));
-          }
-#pragma unroll
-          for (int t = 0; t < ST; ++t) {
-            f32x4 a = zero4();
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) a = mfma16h(r.qt[t][kb], oh[kb], a);
-            Qst[buf][t][lane] = a;
-          }
-        } else {
-          const int jc = nc - 1 - j;
-          const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
-          const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
-          Gst[buf][0][lane] = eg;
-          Gst[buf][1][lane] = __expf(GL - r.G);
-          if (lane == L - 1) Egl[buf] = eg;
-#pragma unroll
-          for (int ti = 0; ti < 4; ++ti) {
-            f32x4 pd = mfma16(r.pt[tb_slot(ti, 1)], dof[1], zero4());
-            if (ti < 2) pd = mfma16(r.pt[tb_slot(ti, 0)], dof[0], pd);
-            Pst[buf][ti][lane] = pd;
-          }
-        }
-      };
-      if (nc > 0) {
-        load(rA, 0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        publish(rA, 0);
-        load(rB, min(1, nc - 1));
-        load(rA, min(2, nc - 1));
-      }
-      __syncthreads();
-      // step j works on register set (j + 1) % 2
-      auto hstep = [&](int j, Regs& r) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kStep));   // step j+1's operands
-        if (j + 1 < nc) publish(r, j + 1);
-        load(r, min(j + 3, nc - 1));
-        __syncthreads();
-      };
-      int j = 0;
-      for (; j + 1 < nc; j += 2) {
-        hstep(j, rB);
-        hstep(j + 1, rA);
-      }
-      if (j < nc) hstep(j, rB);
-    };
-    if (w == 3) helper(std::true_type{});
-    else helper(std::false_type{});
   } else {
-    // ------------------------------------------------------- save wave ----
-    // Step j-1's dS' and dd during step j (their LDS buffers live until
-    // step j+2 overwrites them): the stores have a wave of their own, off the
-    // helper waves, which set the step.
+    // ---------------------------------------------------- helper waves ----
+    // Wave 2 forms step j+1's gate factors and P^T dO into LDS; waves 3 and
+    // 4 form step j+1's Q^T (c' e^G dO), state tiles [0, ST/2) and [ST/2,
+    // ST), and wave 4 also stores step j-1's dS' and dd (their LDS buffers
+    // live until step j+2 overwrites them).  Each uses the register set it
+    // loaded two steps before and then loads step j+3's operands into it.
+    // Every step issues the same loads and stores, so each wait names an
+    // exact count; one code path per role (a compile-time value), so that no
+    // join of two roles' loads blurs the compiler's wait counts.
     typedef unsigned int u32x4l __attribute__((ext_vector_type(4)));
-    // step j's dS' (dse[chunk][v-head] = dS'^T, [V][K], bf16) and dd
-    // (token-major)
+    // step j's dS' (dse[chunk][v-head] = dS'^T, [V][K], bf16) and dd; live =
+    // false (no step yet) stores to empty resources
     auto save = [&](int j, bool live) {
       const int jc = nc - 1 - j;
       const int t0 = s + jc * kChunk, L = live ? min(kChunk, e - t0) : 0;
@@ -437,12 +326,132 @@ __global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d1), dr,
                                              ((2 * vt + 1) * 64 + lane) * 16, 0, 0);
     };
-    __syncthreads();
-    for (int j = 0; j < nc; ++j) {
-      if (j >= 1) save(j - 1, true);
+    auto helper = [&](auto rolec) {
+      constexpr int role = decltype(rolec)::value;
+      constexpr int QT = ST / 2;                 // Q^T state tiles per Q wave
+      constexpr int t_lo = role == 2 ? QT : 0;   // this Q wave's first tile
+      constexpr int kStep = role == 0 ? 6 + 1 : 2 * QT + 1 + (role == 2 ? KB + 2 : 0);
+      struct Regs {
+        u16x8 pt[6];        // P^T fragments (rho rows, bf16) by tb_slot (wave 2)
+        u16x8 qt[QT][2];    // Q^T fragments (rho key rows, fp16) by token k-block
+        float G;            // G of token `lane`
+      };
+      Regs rA, rB;
+      auto load = [&](Regs& r, int j) {
+        const int ci = c_begin + nc - 1 - j;
+        if constexpr (role != 0) {
+          const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+              ws.qtfrag + ((size_t)ci * Hqk + hq) * ST * 128, 0, ST * 128 * 16, kBufferFlags);
+#pragma unroll
+          for (int t = 0; t < QT; ++t) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+              r.qt[t][b] = __builtin_bit_cast(
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                             rq, ((2 * (t_lo + t) + b) * 64 + lane) * 16, 0, 0));
+          }
+        } else {
+          const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+              ws.ptfrag + ((size_t)ci * Hv + h) * 4 * 128, 0, 4 * 128 * 16, kBufferFlags);
+#pragma unroll
+          for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+              if (b == 0 && ti >= 2) continue;
+              r.pt[tb_slot(ti, b)] = __builtin_bit_cast(
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, ((2 * ti + b) * 64 + lane) * 16, 0, 0));
+            }
+          }
+        }
+        const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+            ws.gate + ((size_t)ci * Hv + h) * 64, 0, 256, kBufferFlags);
+        r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
+      };
+      // step j's gate factors and P^T dO (wave 2) or Q^T (c' e^G dO) (waves
+      // 3, 4) into buffer j % 3
+      auto publish = [&](const Regs& r, int j) {
+        const int buf = j % 3;
+        const float eg = __expf(r.G);
+        // dO B fragments: element i of lane (r16, grp), k-block kb is
+        // dO[32 kb + 8 grp + i][16 vt + r16] (the stage wave's tile)
+        u16x8 dof[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) dof[kb] = lds_colfrag(&Dst[j % 4][0][0], 16, 32 * kb, 0, lane);
+        if constexpr (role != 0) {
+          // c' e^G dO for this lane's k-slots (tokens 32 kb + 8 grp + i), fp16;
+          // c' e^G of the tokens through this wave's own LDS row (written and
+          // read back by the one wave, in order)
+          float* eq = Eq[role - 1];
+          eq[lane] = scale * eg;
+          u16x8 oh[2];
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            const f32x4 e0 = *reinterpret_cast<const f32x4*>(&eq[32 * kb + 8 * grp]);
+            const f32x4 e1 = *reinterpret_cast<const f32x4*>(&eq[32 * kb + 8 * grp + 4]);
+            f32x4 x0, x1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              x0[i] = e0[i] * bf2f(dof[kb][i]);
+              x1[i] = e1[i] * bf2f(dof[kb][4 + i]);
+            }
+            oh[kb] = cat8(f2h4(x0), f2h4(x1));
+          }
+#pragma unroll
+          for (int t = 0; t < QT; ++t) {
+            f32x4 a = zero4();
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) a = mfma16h(r.qt[t][kb], oh[kb], a);
+            Qst[buf][t_lo + t][lane] = a;
+          }
+        } else {
+          const int jc = nc - 1 - j;
+          const int t0 = s + jc * kChunk, L = min(kChunk, e - t0);
+          const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
+          Gst[buf][0][lane] = eg;
+          Gst[buf][1][lane] = __expf(GL - r.G);
+          if (lane == L - 1) Egl[buf] = eg;
+#pragma unroll
+          for (int ti = 0; ti < 4; ++ti) {
+            f32x4 pd = mfma16(r.pt[tb_slot(ti, 1)], dof[1], zero4());
+            if (ti < 2) pd = mfma16(r.pt[tb_slot(ti, 0)], dof[0], pd);
+            Pst[buf][ti][lane] = pd;
+          }
+        }
+      };
+      if (nc > 0) load(rA, 0);
+      __syncthreads();   // step 0's dO is in
+      if (nc > 0) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        publish(rA, 0);
+        load(rB, min(1, nc - 1));
+        if constexpr (role == 2) save(0, false);   // the stores a step issues, dropped
+        load(rA, min(2, nc - 1));
+      }
       __syncthreads();
-    }
-    if (nc > 0) save(nc - 1, true);
+      // step j works on register set (j + 1) % 2
+      auto hstep = [&](int j, Regs& r) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kStep));   // step j+1's operands
+        if (j + 1 < nc) publish(r, j + 1);
+        if constexpr (role == 2) save(j - 1, j >= 1);
+        load(r, min(j + 3, nc - 1));
+        __syncthreads();
+      };
+      int j = 0;
+      for (; j + 1 < nc; j += 2) {
+        hstep(j, rB);
+        hstep(j + 1, rA);
+      }
+      if (j < nc) hstep(j, rB);
+      if constexpr (role == 2) {
+        if (nc > 0) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+          save(nc - 1, true);
+        }
+      }
+    };
+    if (w == 2) helper(std::integral_constant<int, 0>{});
+    else if (w == 3) helper(std::integral_constant<int, 1>{});
+    else helper(std::integral_constant<int, 2>{});
   }
 }
 
