@@ -324,12 +324,12 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     // with both outputs, the saves go to a wave of their own (the last)
     constexpr bool kSplit = SAVE && OUT;
     constexpr int kSave = SAVE && !kSplit ? NS * (KB + 2) : 0;   // state and delta stores per chunk
-    constexpr int kStep = (OUT ? 4 * NS : 0) + kSave + kQP + kVG;   // stores + loads per step
+    constexpr int kStep = (OUT ? 2 * NS : 0) + kSave + kQP + kVG;   // stores + loads per step
     // The stores of a step (o tiles, or the saves) go after its loads, and
     // the step's wait lets the previous step's stores stay in flight as well
     // (the counter retires loads and stores in issue order): the stores then
     // have two steps to drain instead of one
-    constexpr int kStores = (OUT ? 4 * NS : 0) + kSave;
+    constexpr int kStores = (OUT ? 2 * NS : 0) + kSave;
     constexpr int kWait = kStep + kStores;
     struct Regs {
       u16x8 qf[4][KB];   // Q rows 16 ti + r16, B operand of (Q S)^T
@@ -469,17 +469,33 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
         }
       }
     };
+    // Tiles 2p and 2p + 1 go out as one 16-byte store per lane: lanes of
+    // even grp keep row 16 (2p) + r16 and take the next 4 columns from their
+    // partner (lane ^ 16), lanes of odd grp keep row 16 (2p + 1) + r16 and
+    // take the 4 columns before theirs (two stores per step instead of four)
     auto out_store = [&](const OutTile& ot, int j, bool live) {
       const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
           o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+      const bool odd = grp & 1;
 #pragma unroll
       for (int sl = 0; sl < NS; ++sl) {
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti)
-          __builtin_amdgcn_raw_buffer_store_b64(
-              __builtin_bit_cast(u32x2, ot.v[sl][ti]), orsrc,
-              (((16 * ti + r16) * Hv + h) * V + 16 * (vt0 + sl) + 4 * grp) * 2, 0, 0);
+        for (int p2 = 0; p2 < 2; ++p2) {
+          const u32x2 mine0 = __builtin_bit_cast(u32x2, ot.v[sl][2 * p2]);
+          const u32x2 mine1 = __builtin_bit_cast(u32x2, ot.v[sl][2 * p2 + 1]);
+          const u32x2 give = odd ? mine0 : mine1;
+          u32x2 got;
+          got[0] = __shfl_xor(give[0], 16);
+          got[1] = __shfl_xor(give[1], 16);
+          const u32x4 row = odd ? u32x4{got[0], got[1], mine1[0], mine1[1]}
+                                : u32x4{mine0[0], mine0[1], got[0], got[1]};
+          __builtin_amdgcn_raw_buffer_store_b128(
+              row, orsrc,
+              (((16 * (2 * p2 + (odd ? 1 : 0)) + r16) * Hv + h) * V + 16 * (vt0 + sl) +
+               4 * (grp & 2)) * 2,
+              0, 0);
+        }
       }
     };
     if (kSplit && w == NS + 2) {
