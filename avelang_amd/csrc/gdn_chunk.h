@@ -154,19 +154,24 @@ __device__ __forceinline__ constexpr int vmcnt_imm(int n) {
   return 0x0F70 | (n & 15) | (((n >> 4) & 3) << 14);
 }
 
-// Staged K rows: row stride 2K + 16 bytes and 64 more bytes after every 16
-// rows.  The column-fragment reads of the state wave (16 rows rho(16 ti +
-// m), one 16-byte piece) then fall on distinct banks, and every K read is a
-// per-lane base plus a compile-time offset.
+// Staged K rows: 2K bytes per row, unpadded, the row's 16-byte units
+// (8 keys each) permuted by XOR with swz(row), which takes row bits 3-4 to
+// unit bits 0-1 and row bits 0-1 (K = 128; bit 1 for K = 64) to the unit
+// bits above.  Both fragment reads of the state wave then fall on distinct
+// banks across each 16 lanes: the column-fragment reads (16 rows rho(16 ti
+// + m), one unit) and the transposing reads (4 rows x 4 units); row bits 2
+// and 5 do not enter swz, so every K read is one of a few per-lane bases
+// plus a compile-time offset.
 template <int K>
 struct KLayout {
-  static constexpr int RS = 2 * K + 16;            // row stride (bytes)
-  static constexpr int GP = 64;                    // extra bytes per 16 rows
-  static constexpr int GU = (16 * RS + GP) / 16;   // 16-byte units per 16 rows
-  static constexpr int UNITS = 4 * GU;             // units of the 64 rows
-  static constexpr int LOADS = (UNITS + 63) / 64;  // 1 KiB direct-to-LDS loads
-  static constexpr int BYTES = LOADS * 1024;       // buffer size
-  __device__ static constexpr int row(int r) { return r * RS + (r >> 4) * GP; }
+  static constexpr int RS = 2 * K;                 // row stride (bytes)
+  static constexpr int BYTES = 64 * RS;            // buffer size
+  static constexpr int LOADS = BYTES / 1024;       // 1 KiB direct-to-LDS loads
+  __device__ static constexpr int swz(int r) {
+    return ((r >> 3) & 3) | ((K == 128 ? (r & 3) : ((r >> 1) & 1)) << 2);
+  }
+  // byte offset of unit u (keys 8u .. 8u + 7) of row r
+  __device__ static constexpr int off(int r, int u) { return r * RS + 16 * (u ^ swz(r)); }
 };
 
 // Workspace plan (byte offsets into the caller's buffer).

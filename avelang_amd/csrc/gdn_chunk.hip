@@ -269,10 +269,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     if (h % (Hv / Hqk) == 0) {
       using KL = KLayout<K>;
       const int row = 16 * w + r16;
-      unsigned char* kd = ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES + KL::row(row);
+      unsigned char* kd = ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES;
 #pragma unroll
       for (int b = 0; b < KB; ++b)
-        *reinterpret_cast<u16x8*>(kd + 16 * (4 * b + grp)) =
+        *reinterpret_cast<u16x8*>(kd + KL::off(row, 4 * b + grp)) =
             row < L ? bf2h8(ka[b]) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
       if constexpr (OUT) {
         u16x8* qd = ws.q16 + (((size_t)ci * Hqk + hq) * 4 + w) * KB * 64 + lane;

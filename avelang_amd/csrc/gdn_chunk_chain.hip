@@ -121,16 +121,18 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     }
     __syncthreads();   // stage buffer 0 is filled
 
-    // per-lane byte offsets into a K stage buffer: K A fragments (row
-    // rho(16 ti + r16), piece grp; k-block b adds 64 b) and the transposing
-    // reads of K^T (rows 8 grp + m4 and 8 grp + 4 + m4, piece q4; k-block b
-    // adds 32 rows, state tile t adds 4 (t / 2) pieces and 8 (t % 2) bytes)
+    // per-lane byte offsets into a K stage buffer (KLayout): K A fragments
+    // of k-block b (row rho(16 ti + r16), unit 4 b + grp; tile ti adds
+    // rows 32 (ti / 2) + 4 (ti % 2), which leave swz unchanged) and the
+    // transposing reads of K^T for state tiles 2u, 2u + 1 (row 8 grp + m4,
+    // unit 4 u + q4; the second 4 rows, k-block b's 32 rows and 8 (t % 2)
+    // bytes are compile-time offsets)
     const int m4 = r16 >> 2, q4 = r16 & 3;
-    int ka_off[4];
+    int ka_off[KB], tr_off[ST / 2];
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) ka_off[ti] = KL::row(rho_row(ti, r16)) + 16 * grp;
-    const int tr_lo = KL::row(8 * grp + m4) + 16 * q4;
-    const int tr_hi = KL::row(8 * grp + 4 + m4) + 16 * q4;
+    for (int b = 0; b < KB; ++b) ka_off[b] = KL::off(rho_row(0, r16), 4 * b + grp);
+#pragma unroll
+    for (int u = 0; u < ST / 2; ++u) tr_off[u] = KL::off(8 * grp + m4, 4 * u + q4);
 
     // one chunk step on stage / output buffer B3 (a compile-time index, so
     // that every LDS address is a per-lane base plus an immediate)
@@ -146,7 +148,8 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       for (int b = 0; b < KB; ++b) {
 #pragma unroll
         for (int ti = 0; ti < 4; ++ti)
-          ka[b][ti] = *reinterpret_cast<const u16x8*>(Kb + ka_off[ti] + 64 * b);
+          ka[b][ti] = *reinterpret_cast<const u16x8*>(
+              Kb + ka_off[b] + KL::RS * (32 * (ti >> 1) + 4 * (ti & 1)));
       }
 #pragma unroll
       for (int i = 0; i < 6; ++i) ta[i] = Tst[b3][i][lane];
@@ -203,9 +206,9 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int t = 0; t < ST; ++t) {
-          const int imm = KL::row(32 * b) + 64 * (t >> 1) + 8 * (t & 1);
-          const u16x4 lo4 = lds_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_lo + imm));
-          const u16x4 hi4 = lds_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_hi + imm));
+          const unsigned char* p = Kb + tr_off[t >> 1] + KL::RS * 32 * b + 8 * (t & 1);
+          const u16x4 lo4 = lds_tr16(reinterpret_cast<const uint16_t*>(p));
+          const u16x4 hi4 = lds_tr16(reinterpret_cast<const uint16_t*>(p + KL::RS * 4));
           kt[b][t] = cat8(lo4, hi4);
         }
       }

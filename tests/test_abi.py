@@ -147,9 +147,9 @@ def test_workspace_bytes_grow_with_problem(lib):
     # prep kernel's fp16 copies of K and Q either way
     assert 0 < a < b and c > a and d == a
     # per (chunk, v-head): 64 gate floats (G) + 6 KiB Tb + 6 KiB P fragments;
-    # per (chunk, qk-head): the fp16 K block (18 KiB with its LDS padding)
-    # and the fp16 Q fragments (16 KiB)
-    assert a >= 128 * 32 * (256 + 6144 + 6144) + 128 * 16 * (18432 + 16384)
+    # per (chunk, qk-head): the fp16 K block (16 KiB: 64 unpadded rows, their
+    # 16-byte units permuted) and the fp16 Q fragments (16 KiB)
+    assert a >= 128 * 32 * (256 + 6144 + 6144) + 128 * 16 * (16384 + 16384)
     # the backward's workspace keeps the normalised rows with l2norm
     bw = lib.gdn_chunk_bwd_workspace_bytes
     assert bw(1, 8192, 16, 32, 128, 128, 1, 0, 1) > bw(1, 8192, 16, 32, 128, 128, 1, 0, 0)
