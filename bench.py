@@ -5,10 +5,12 @@
 Headline (``value``): config 1, Qwen3-Next GDN chunked prefill (B=1,
 T=8192, 16 qk-heads -> 32 v-heads, K=V=128, bf16 q/k/v, fp32 g/beta/state,
 initial state, output_final_state=True) in tokens/s.  A step is one
-``chunk_gated_delta_rule`` call over the whole 8192-token batch; its HIP
-graph (one capture of the call) is replayed K times between two
-``torch.cuda.synchronize()`` calls and timed with events on the stream the
-kernels run on.  Inputs are resident in HBM before timing starts.
+``chunk_gated_delta_rule`` call over the whole 8192-token batch, launched
+eagerly K times in a row between two ``torch.cuda.synchronize()`` calls and
+timed with events on the stream the kernels run on (the host enqueues a call
+in far less time than the GPU runs it, so the kernels run back to back;
+``host_enqueue_ms_per_step`` reports it).  Inputs are resident in HBM before
+timing starts.
 
 Secondary (``decode``): config 2, batch-256 fused-recurrent decode with the
 fp32 state [256, 32, 128, 128] updated in place, 1000 consecutive steps
@@ -22,8 +24,12 @@ launch (20 launches in one HIP graph, median of 5 replays).
 
 ``cpu_baseline``: the C/OpenMP fp32 oracle (oracle/gdn_cpu.c, a port, not the
 reference: the reference has no GDN code) timed on this host's cores.
-Methodology mirrors the reference's GEMM benchmark
-(benchmark/gemm/bench_amdgpu_gemm.py:36-52: warm up, capture, replay, events).
+Methodology follows the reference's GEMM benchmark
+(benchmark/gemm/bench_amdgpu_gemm.py:36-52: warm up, then events around the
+timed launches), the decode and backward lines replaying HIP graphs of
+several calls; the headline launches eagerly, because replaying a graph of
+one call per step adds ~5 us of graph-launch turnover between steps (0.176
+against 0.171 ms per call on one box; a graph of four calls measures 0.172).
 """
 from __future__ import annotations
 
@@ -104,32 +110,23 @@ def bench_prefill(dev, steps, warmup, l2norm=False):
                                workspace=ws, out=o, final_state=ht,
                                use_qk_l2norm_in_kernel=l2norm)
 
-    side = torch.cuda.Stream(device=dev)
-    side.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(side):
-        for _ in range(3):
-            call()
-    torch.cuda.current_stream(dev).wait_stream(side)
-    torch.cuda.synchronize(dev)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        call()
     for _ in range(warmup):
-        graph.replay()
+        call()
     torch.cuda.synchronize(dev)
     stream = torch.cuda.current_stream(dev)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(dev)
     w0 = time.perf_counter()
     e0.record(stream)
     for _ in range(steps):
-        graph.replay()
+        call()
     e1.record(stream)
+    enq = time.perf_counter() - w0
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - w0
     ms = e0.elapsed_time(e1) / steps
-    return dict(ms=ms, wall_ms=wall * 1e3 / steps, T=T, Hv=Hv, K=K, V=V, wl=wl)
+    return dict(ms=ms, wall_ms=wall * 1e3 / steps, enqueue_ms=enq * 1e3 / steps, T=T, Hv=Hv,
+                K=K, V=V, wl=wl)
 
 
 def bench_backward(dev, steps, warmup):
@@ -763,6 +760,7 @@ def main():
         "layer_ops": layer,
         "fusions": fusions,
         "host_wall_ms_per_step": round(pre["wall_ms"], 5),
+        "host_enqueue_ms_per_step": round(pre["enqueue_ms"], 5),
     }
     print(json.dumps(rec), flush=True)
 
