@@ -24,6 +24,7 @@ struct ChunkWs {
                        // the chain's LDS layout (rows past the sequence end 0)
   u16x8* q16;       // [NC][Hqk][4 row tiles][K/32 k-blocks][64] fp16 B-operand
                     // fragments of the chunk's Q rows (forms that write o)
+                    // (k16 / q16 NULL where the plan has no such copy: WsPlan)
   uint16_t* qn;     // l2-normalised q, k rows [B*T][Hqk][K] bf16 (use_qk_l2norm with
   uint16_t* kn;     // the backward), written by the prep kernel
   // backward only
@@ -174,9 +175,23 @@ struct KLayout {
   __device__ static constexpr int off(int r, int u) { return r * RS + 16 * (u ^ swz(r)); }
 };
 
+// Whether a chunked call's forward chain reads K from the caller's bf16 rows
+// (a convert wave, one V tile per workgroup) rather than the prep kernel's
+// fp16 copy: a forward without use_qk_l2norm whose chains do not fill the
+// GPU twice over (the backward's reverse chain reads the copy, and two V
+// tiles per workgroup leave no registers for the convert wave).  Q is read
+// from the caller's rows whenever use_qk_l2norm is off.
+inline bool chain_two_tiles(int N, int Hv, int V) {
+  return V % 32 == 0 && (long long)N * Hv * (V / 16) >= 2LL * device_cus();
+}
+inline bool chain_reads_rows(bool bwd, bool l2, int N, int Hv, int V) {
+  return !bwd && !l2 && !chain_two_tiles(N, Hv, V);
+}
+
 // Workspace plan (byte offsets into the caller's buffer).
 struct WsPlan {
   size_t off, status, gate, tfrag, pfrag, k16, q16, qn, kn, total;
+  bool k16_copy, q16_copy;   // k16 / q16 planned (else the chains read the caller's rows)
   // backward only (0 when not planned)
   size_t tmat, ttfrag, ptfrag, qtfrag, hs, dl, dse, dd;
   long long ncmax;
@@ -201,10 +216,13 @@ ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb);
 
 // Forward chain, state-wave form (gdn_chunk_chain.hip).  SAVE: the state at
 // every chunk start and the per-token deltas for the backward; OUT: o, ht.
+// qraw, kraw (a forward, OUT without SAVE, both non-null): K and Q from the
+// caller's bf16 rows instead of ws.k16 / ws.q16.
 template <int K, bool SAVE, bool OUT>
-void launch_chain_sw(const uint16_t* v, const float* h0, float* ht, uint16_t* o,
-                     const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
-                     float scale, const ChunkWs& ws, hipStream_t st);
+void launch_chain_sw(const uint16_t* v, const uint16_t* qraw, const uint16_t* kraw,
+                     const float* h0, float* ht, uint16_t* o, const int32_t* cu, int N, int T,
+                     int total, int Hqk, int Hv, int V, float scale, const ChunkWs& ws,
+                     hipStream_t st);
 
 // Reverse chain of the backward (gdn_chunk_rev.hip): dS' of every chunk into
 // dse, dd into dd, dh0 (K rows from ws.k16).

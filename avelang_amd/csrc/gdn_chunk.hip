@@ -265,8 +265,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     // in the chain's LDS layout with rows past the sequence end zeroed, so
     // the chain copies it to LDS with contiguous loads; Q as the B-operand
     // fragments the chain's output wave loads (row 16 w + r16, columns
-    // 32 b + 8 grp ..).
-    if (h % (Hv / Hqk) == 0) {
+    // 32 b + 8 grp ..).  Not when the plan has no copies (the chain reads
+    // the caller's rows).
+    if (ws.k16 && h % (Hv / Hqk) == 0) {
       using KL = KLayout<K>;
       const int row = 16 * w + r16;
       unsigned char* kd = ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES;
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       for (int b = 0; b < KB; ++b)
         *reinterpret_cast<u16x8*>(kd + KL::off(row, 4 * b + grp)) =
             row < L ? bf2h8(ka[b]) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      if constexpr (OUT) {
+      if (OUT && ws.q16) {
         u16x8* qd = ws.q16 + (((size_t)ci * Hqk + hq) * 4 + w) * KB * 64 + lane;
 #pragma unroll
         for (int b = 0; b < KB; ++b) qd[b * 64] = bf2h8(qa[b]);
@@ -518,9 +519,14 @@ WsPlan plan_ws(int B, int T, int Hqk, int Hv, int K, int V, int N, bool has_cu, 
   p.gate = take(nch * 64 * 4);
   p.tfrag = take(nch * 6 * 64 * 16);
   p.pfrag = take(nch * 6 * 64 * 16);
+  // the fp16 K / Q copies, where the chains do not read the caller's rows:
+  // Q only with use_qk_l2norm (normalised), K also for the backward and for
+  // two V tiles per workgroup
   const size_t nqk = (size_t)p.ncmax * Hqk;   // (chunk, qk-head) pairs
-  p.k16 = take(nqk * (K == 128 ? KLayout<128>::BYTES : KLayout<64>::BYTES));
-  p.q16 = take(nqk * 64 * K * 2);
+  p.k16_copy = !chain_reads_rows(bwd, l2, N, Hv, V);
+  p.q16_copy = l2;
+  p.k16 = take(p.k16_copy ? nqk * (K == 128 ? KLayout<128>::BYTES : KLayout<64>::BYTES) : 0);
+  p.q16 = take(p.q16_copy ? nqk * 64 * K * 2 : 0);
   p.qn = p.kn = at;
   if (l2 && bwd) {
     p.qn = take((size_t)total * Hqk * K * 2);
@@ -547,8 +553,8 @@ ChunkWs ws_pointers(const WsPlan& p, unsigned char* wsb) {
   ws.gate = reinterpret_cast<float*>(wsb + p.gate);
   ws.tfrag = reinterpret_cast<u16x8*>(wsb + p.tfrag);
   ws.pfrag = reinterpret_cast<u16x8*>(wsb + p.pfrag);
-  ws.k16 = wsb + p.k16;
-  ws.q16 = reinterpret_cast<u16x8*>(wsb + p.q16);
+  ws.k16 = p.k16_copy ? wsb + p.k16 : nullptr;
+  ws.q16 = p.q16_copy ? reinterpret_cast<u16x8*>(wsb + p.q16) : nullptr;
   ws.qn = reinterpret_cast<uint16_t*>(wsb + p.qn);
   ws.kn = reinterpret_cast<uint16_t*>(wsb + p.kn);
   if (p.hs) {
@@ -581,10 +587,11 @@ static void launch_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v
       hipLaunchKernelGGL((chunk_prep_kernel<K, BWD, OUT, false>), dim3((unsigned)p.ncmax, Hv), dim3(256),
                          0, st, q, k, g, beta, cu, N, T, total, Hqk, Hv, scale, ws, gate);
   }
-  // the chain reads K and Q as the prep kernel's fp16 copies (normalised
-  // with use_qk_l2norm)
-  launch_chain_sw<K, BWD, OUT>(v, h0, OUT ? ht : nullptr, OUT ? o : nullptr, cu, N, T, total,
-                               Hqk, Hv, V, scale, ws, st);
+  // the chain reads K and Q as the prep kernel's fp16 copies where the plan
+  // has them (normalised with use_qk_l2norm), else as the caller's bf16 rows
+  launch_chain_sw<K, BWD, OUT>(v, ws.q16 ? nullptr : q, ws.k16 ? nullptr : k, h0,
+                               OUT ? ht : nullptr, OUT ? o : nullptr, cu, N, T, total, Hqk, Hv,
+                               V, scale, ws, st);
   // a cu_seqlens violation left every sequence empty: o is zero-filled (and
   // ht = h0, written by the chain for an empty sequence)
   if (cu && OUT) {

@@ -50,11 +50,30 @@ namespace gdn {
 // workgroup, one state wave each, sharing the stage wave's K / Tb buffers
 // and the output wave's Q / P (2 when there are enough chains to fill the
 // GPU twice over).
-template <int K, bool SAVE, bool OUT, int NS>
-__global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_chain_sw_kernel(
-    const uint16_t* __restrict__ v, const float* h0, float* ht, uint16_t* __restrict__ o,
-    const int32_t* __restrict__ cu, int N, int T, int total, int Hqk, int Hv, int V,
-    float scale, ChunkWs ws) {
+//
+// Without use_qk_l2norm the chain reads the caller's bf16 rows where the
+// prep kernel would otherwise have to copy them:
+// RAWQ (forms with OUT): the output wave takes Q S on bf16 MFMA, Q rows
+//   loaded as they are and the state's fp16 fragments re-rounded to bf16 --
+//   the rounding the operator's bf16 contract allows there, while the state's
+//   own products keep fp16 (the prep writes no fp16 Q copy).  The state wave
+//   publishes the same fp16 fragments in every form, so the backward's saved
+//   states do not depend on it.
+// RAWK (a plain forward, one V tile per workgroup): a fourth (convert) wave
+//   loads chunk c+2's K rows into its registers during step c and writes
+//   chunk c+1's, converted, as the fp16 KLayout block (rows past the
+//   sequence end 0); the prep writes no fp16 K copy.  (The backward's chains
+//   and two V tiles per workgroup keep the copy: the reverse chain reads it
+//   too, and the convert wave's registers would not fit beside two state
+//   waves.)
+template <int K, bool SAVE, bool OUT, int NS, bool RAWK, bool RAWQ>
+__global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0) + (RAWK ? 1 : 0)) * 64) void
+chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict__ qraw,
+                      const uint16_t* __restrict__ kraw, const float* h0, float* ht,
+                      uint16_t* __restrict__ o, const int32_t* __restrict__ cu, int N, int T,
+                      int total, int Hqk, int Hv, int V, float scale, ChunkWs ws) {
+  static_assert(!RAWK || (OUT && !SAVE && NS == 1 && RAWQ), "RAWK is a plain forward");
+  static_assert(!RAWQ || OUT, "RAWQ forms o");
   constexpr int KB = K / 32;   // k-blocks over the key index
   constexpr int ST = K / 16;   // 16-row state tiles
   // Stage buffers (chunk c in buffer c % 3): the chunk's K rows (KLayout),
@@ -263,20 +282,22 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     // fence would wait for the loads still in flight for the next step),
     // with signal fences so that no LDS access moves across them.
     typedef __attribute__((address_space(3))) void* lds_ptr;
-    constexpr int kKT = KL::LOADS + 6 + 2 * NS;  // loads per stage: K, Tb, V tiles
+    constexpr int kKT = (RAWK ? 0 : KL::LOADS) + 6 + 2 * NS;  // loads per stage: K, Tb, V tiles
     // chunk j's data into buffer jb % 3 (past the last chunk the loads repeat
     // it into a buffer no step reads, which keeps every step's count equal):
     // the prep kernel's fp16 K block (already in KLayout, rows past the
-    // sequence end zero) and Tb fragments (already in rho row order), both
-    // contiguous, so lane l of load i copies bytes 16 (64 i + l)
+    // sequence end zero; not with RAWK) and Tb fragments (already in rho row
+    // order), both contiguous, so lane l of load i copies bytes 16 (64 i + l)
     auto issue_kt = [&](int j, int jb) {
       const int ci = c_begin + j, buf = jb % 3;
-      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES, 0, KL::BYTES, kBufferFlags);
+      if constexpr (!RAWK) {
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            ws.k16 + ((size_t)ci * Hqk + hq) * KL::BYTES, 0, KL::BYTES, kBufferFlags);
 #pragma unroll
-      for (int i = 0; i < KL::LOADS; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(Kst[buf] + 1024 * i), 16,
-                                                 1024 * i + 16 * lane, 0, 0, 0);
+        for (int i = 0; i < KL::LOADS; ++i)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(Kst[buf] + 1024 * i), 16,
+                                                   1024 * i + 16 * lane, 0, 0, 0);
+      }
       const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
           ws.tfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
 #pragma unroll
@@ -314,6 +335,64 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(kKT));   // chunk j+1
       barrier();
     }
+  } else if (RAWK && w == NS + 2) {
+    // ---------------------------------------------------- convert wave ----
+    // During step j: loads chunk j+2's bf16 K rows into register set j % 2
+    // (load i, lane l: 16 bytes l % (K / 8) of row (64 / (K / 8)) i + l /
+    // (K / 8); rows past the sequence end read as 0), waits for chunk j+1's
+    // (issued during step j-1) and writes them, as fp16, into chunk j+1's
+    // KLayout block (rows past the end 0: the state update K^T U must not see
+    // them); before step 0, chunk 0's.  Its LDS traffic is that block only.
+    constexpr int UPR = K / 8, RPL = 64 / UPR;
+    typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+    u32x4v xa[KL::LOADS], xb[KL::LOADS];
+    auto load = [&](u32x4v (&x)[KL::LOADS], int c) {
+      const int t0 = s + c * kChunk, L = min(kChunk, e - t0);
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(kraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
+          kBufferFlags);
+#pragma unroll
+      for (int i = 0; i < KL::LOADS; ++i)
+        x[i] = __builtin_amdgcn_raw_buffer_load_b128(
+            rk, (RPL * i + lane / UPR) * Hqk * K * 2 + 16 * (lane % UPR), 0, 0);
+    };
+    auto convert = [&](const u32x4v (&x)[KL::LOADS], int c) {
+      const int t0 = s + c * kChunk, L = min(kChunk, e - t0);
+      unsigned char* dst = Kst[c % 3];
+      if (L == kChunk) {   // a whole chunk: nothing to mask
+#pragma unroll
+        for (int i = 0; i < KL::LOADS; ++i)
+          *reinterpret_cast<u32x4v*>(dst + KL::off(RPL * i + lane / UPR, lane % UPR)) =
+              __builtin_bit_cast(u32x4v, bf2h8(__builtin_bit_cast(u16x8, x[i])));
+      } else {
+#pragma unroll
+        for (int i = 0; i < KL::LOADS; ++i) {
+          const int row = RPL * i + lane / UPR, u = lane % UPR;
+          const unsigned keep = row < L ? 0xFFFFFFFFu : 0u;
+          *reinterpret_cast<u32x4v*>(dst + KL::off(row, u)) =
+              __builtin_bit_cast(u32x4v, bf2h8(__builtin_bit_cast(u16x8, x[i]))) & keep;
+        }
+      }
+    };
+    if (nc > 0) {
+      load(xa, 0);
+      load(xb, min(1, nc - 1));
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(KL::LOADS));   // chunk 0
+      convert(xa, 0);
+    }
+    __syncthreads();
+    auto step = [&](int j, u32x4v (&mine)[KL::LOADS], u32x4v (&next)[KL::LOADS]) {
+      load(mine, min(j + 2, nc - 1));
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(KL::LOADS));   // chunk j+1
+      if (j + 1 < nc) convert(next, j + 1);
+      __syncthreads();
+    };
+    int j = 0;
+    for (; j + 1 < nc; j += 2) {
+      step(j, xa, xb);
+      step(j + 1, xb, xa);
+    }
+    if (j < nc) step(j, xa, xb);
   } else {
     // ----------------------------------------------------- output wave ----
     // During step j: writes chunk j+1's gate factors into stage buffer
@@ -345,14 +424,31 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
     auto load_qp = [&](Regs& r, int j) {
       if constexpr (!OUT) return;
       const int ci = c_begin + j;
-      const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-          ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
+      if constexpr (RAWQ) {
+        // bf16 B fragments straight from q: row 16 ti + r16 of the chunk,
+        // columns 32 b + 8 grp .. + 7 (rows past the sequence end read as 0)
+        const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
+            kBufferFlags);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
+        for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
-        for (int b = 0; b < KB; ++b)
-          r.qf[ti][b] = __builtin_bit_cast(
-              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16, 0, 0));
+          for (int b = 0; b < KB; ++b)
+            r.qf[ti][b] = __builtin_bit_cast(
+                u16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                           rq, ((16 * ti + r16) * Hqk * K + 32 * b + 8 * grp) * 2, 0, 0));
+        }
+      } else {
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+          for (int b = 0; b < KB; ++b)
+            r.qf[ti][b] = __builtin_bit_cast(
+                u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16, 0, 0));
+        }
       }
       const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
           ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
@@ -449,7 +545,10 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
         u16x8 sh[KB], vx[2];
         if (live) {
 #pragma unroll
-          for (int b = 0; b < KB; ++b) sh[b] = Sx[b3][sl][b][lane];
+          for (int b = 0; b < KB; ++b) {
+            sh[b] = Sx[b3][sl][b][lane];
+            if constexpr (RAWQ) sh[b] = h2bf8(sh[b]);   // B of the bf16 Q S
+          }
           vx[0] = Vx[b3][sl][0][lane];
           vx[1] = Vx[b3][sl][1][lane];
         }
@@ -460,8 +559,13 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
             f32x4 qa = zero4(), qb = zero4();
 #pragma unroll
             for (int b = 0; b < KB; b += 2) {
-              qa = mfma16h(sh[b], r.qf[ti][b], qa);
-              qb = mfma16h(sh[b + 1], r.qf[ti][b + 1], qb);
+              if constexpr (RAWQ) {
+                qa = mfma16(sh[b], r.qf[ti][b], qa);
+                qb = mfma16(sh[b + 1], r.qf[ti][b + 1], qb);
+              } else {
+                qa = mfma16h(sh[b], r.qf[ti][b], qa);
+                qb = mfma16h(sh[b + 1], r.qf[ti][b + 1], qb);
+              }
             }
             f32x4 pv = mfma16h(vx[0], r.pf[tb_slot(ti, 0)], zero4());
             if (ti >= 2) pv = mfma16h(vx[1], r.pf[tb_slot(ti, 1)], pv);
@@ -565,29 +669,41 @@ __global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0)) * 64) void chunk_c
 }
 
 template <int K, bool SAVE, bool OUT>
-void launch_chain_sw(const uint16_t* v, const float* h0, float* ht, uint16_t* o,
-                     const int32_t* cu, int N, int T, int total, int Hqk, int Hv, int V,
-                     float scale, const ChunkWs& ws, hipStream_t st) {
+void launch_chain_sw(const uint16_t* v, const uint16_t* qraw, const uint16_t* kraw,
+                     const float* h0, float* ht, uint16_t* o, const int32_t* cu, int N, int T,
+                     int total, int Hqk, int Hv, int V, float scale, const ChunkWs& ws,
+                     hipStream_t st) {
   // two V tiles per workgroup once the chains fill the GPU twice over: the
   // tiles share the stage and output waves' operand traffic, and every chain
   // still has a state wave of its own (not with both outputs: a fifth wave
-  // would halve the register budget)
+  // would halve the register budget; not with RAWK, see above)
   const long long chains = (long long)N * Hv * (V / 16);
   constexpr int kExtra = SAVE && OUT ? 1 : 0;
-  if (!(SAVE && OUT) && V % 32 == 0 && chains >= 2LL * device_cus())
-    hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT, (SAVE && OUT) ? 1 : 2>),
-                       dim3((unsigned)(chains / 2)), dim3((4 + kExtra) * 64), 0, st, v, h0, ht,
-                       o, cu, N, T, total, Hqk, Hv, V, scale, ws);
-  else
-    hipLaunchKernelGGL((chunk_chain_sw_kernel<K, SAVE, OUT, 1>), dim3((unsigned)chains),
-                       dim3((3 + kExtra) * 64), 0, st, v, h0, ht, o, cu, N, T, total, Hqk, Hv,
-                       V, scale, ws);
+  const bool rawq = OUT && qraw;
+  const bool rawk = OUT && !SAVE && rawq && kraw;
+  const bool two = !(SAVE && OUT) && !rawk && chain_two_tiles(N, Hv, V);
+  const dim3 grid((unsigned)(two ? chains / 2 : chains));
+  auto go = [&](auto kern, int waves) {
+    hipLaunchKernelGGL(kern, grid, dim3(waves * 64), 0, st, v, qraw, kraw, h0, ht, o, cu, N, T,
+                       total, Hqk, Hv, V, scale, ws);
+  };
+  if constexpr (OUT) {
+    if constexpr (!SAVE) {
+      if (rawk) return go(chunk_chain_sw_kernel<K, false, true, 1, true, true>, 4);
+    }
+    if (rawq) {
+      if (two) return go(chunk_chain_sw_kernel<K, SAVE, OUT, SAVE ? 1 : 2, false, true>, 4 + kExtra);
+      return go(chunk_chain_sw_kernel<K, SAVE, OUT, 1, false, true>, 3 + kExtra);
+    }
+  }
+  if (two) go(chunk_chain_sw_kernel<K, SAVE, OUT, (SAVE && OUT) ? 1 : 2, false, false>, 4 + kExtra);
+  else go(chunk_chain_sw_kernel<K, SAVE, OUT, 1, false, false>, 3 + kExtra);
 }
 
-#define GDN_CHAIN_INST(K_, SAVE_, OUT_)                                                       \
-  template void launch_chain_sw<K_, SAVE_, OUT_>(const uint16_t*, const float*, float*,     \
-                                                 uint16_t*, const int32_t*, int, int, int, int, \
-                                                 int, int, float, const ChunkWs&, hipStream_t);
+#define GDN_CHAIN_INST(K_, SAVE_, OUT_)                                                     \
+  template void launch_chain_sw<K_, SAVE_, OUT_>(                                           \
+      const uint16_t*, const uint16_t*, const uint16_t*, const float*, float*, uint16_t*,   \
+      const int32_t*, int, int, int, int, int, int, float, const ChunkWs&, hipStream_t);
 GDN_CHAIN_INST(64, false, true)
 GDN_CHAIN_INST(64, true, false)
 GDN_CHAIN_INST(64, true, true)

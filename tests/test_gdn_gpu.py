@@ -296,10 +296,14 @@ def test_prefill_deterministic(rocm_device):
 
 def test_prefill_homogeneous_cfg1(rocm_device):
     """Config 1 in full, no oracle: the recurrence is jointly linear in (h0, v), and every step
-    of the kernels commutes with doubling (fp16 roundings, MFMA products and fp32 sums of doubled
-    operands are the doubled results) except where an fp16 operand falls below fp16's normal
-    range (|x| < 2^-14), whose rounding step is absolute (2^-24).  So doubling h0 and v doubles
-    the final state to ~1e-7 and o to within one bf16 rounding."""
+    of the kernels commutes with doubling (fp16 / bf16 roundings, MFMA products and fp32 sums of
+    doubled operands are the doubled results) except where an fp16 operand falls below fp16's
+    normal range (|x| < 2^-14), whose rounding step is absolute (2^-24).  So doubling h0 and v
+    doubles the final state to ~1e-7, and o to within one bf16 rounding, except where that tiny
+    state difference moves an element of S across a rounding boundary of the bf16 S that Q S
+    takes (this forward reads q and k as the caller's bf16 rows): such a term moves by one bf16
+    step of S times scale q, under 1e-4 here, and it happens rarely (the relative Frobenius
+    difference of o stays ~1e-6)."""
     from avelang_amd import chunk_gated_delta_rule
     t = W.config("cfg1_prefill_qwen3next", seed=21).torch(rocm_device)
     o1, s1 = chunk_gated_delta_rule(t["q"], t["k"], t["v"], t["g"], t["beta"],
@@ -309,7 +313,10 @@ def test_prefill_homogeneous_cfg1(rocm_device):
     torch.cuda.synchronize()
     fro = ((s2 - 2 * s1).norm() / (2 * s1).norm()).item()
     assert fro < 1e-5, fro
-    torch.testing.assert_close(o2.float(), 2 * o1.float(), rtol=2 ** -7, atol=1e-5)
+    torch.testing.assert_close(o2.float(), 2 * o1.float(), rtol=2 ** -7, atol=1e-4)
+    o_fro = ((o2.float() - 2 * o1.float()).norm() / (2 * o1.float()).norm()).item()
+    print(f"homogeneity: state rel fro {fro:.2e}, o rel fro {o_fro:.2e}", flush=True)
+    assert o_fro < 1e-4, o_fro
 
 
 def test_prefill_beta_zero_pure_decay_cfg1(rocm_device):
@@ -395,9 +402,10 @@ def test_golden_cfg0(rocm_device):
 @pytest.mark.parametrize("K,V", [(128, 128), (64, 64)])
 def test_two_tiles_per_workgroup(rocm_device, K, V):
     """With at least twice as many (sequence, v-head, V tile) chains as CUs
-    the chain runs two V tiles per workgroup.  Every sequence matches the
-    oracle, and sequence 0 equals, bit for bit, the same sequence run alone
-    (few chains: one tile per workgroup)."""
+    the chain runs two V tiles per workgroup (K from the prep kernel's fp16
+    copy).  Every sequence matches the oracle, and sequence 0 equals, bit for
+    bit, the same sequence run alone (few chains: one tile per workgroup, K
+    converted from the caller's rows inside the chain, to the same fp16)."""
     from avelang_amd import chunk_gated_delta_rule
     Hqk, Hv = 4, 8
     cus = torch.cuda.get_device_properties(rocm_device).multi_processor_count
