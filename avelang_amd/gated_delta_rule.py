@@ -241,7 +241,7 @@ def chunk_gated_delta_rule_fwd_save(
 # Default of chunk_gated_delta_rule's save_for_backward: the autograd forward
 # keeps the backward's workspace (chunk_bwd_workspace_bytes: chunk-start
 # states, deltas, the prep's fragments and fp16 K / Q copies -- about 160 KB
-# per chunk and v-head, 660 MB for a T = 8192, 32-v-head layer) alive until
+# per chunk and v-head, 622 MB for a T = 8192, 32-v-head layer) alive until
 # the backward, which then skips the forward recomputation.  False: keep
 # only the inputs and recompute (the backward then takes ~0.2 ms more at that
 # shape).
@@ -325,7 +325,7 @@ def chunk_gated_delta_rule(
     ``save_for_backward`` (default: the module's SAVE_FORWARD_FOR_BACKWARD)
     chooses, for that call, between keeping the backward's workspace from
     the forward (``chunk_bwd_workspace_bytes(...)`` bytes held until the
-    backward, 660 MB at T = 8192 with 32 v-heads; the backward skips the
+    backward, 622 MB at T = 8192 with 32 v-heads; the backward skips the
     recomputation) and keeping only the inputs (the backward recomputes).
     """
     if torch.is_grad_enabled() and any(

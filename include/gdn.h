@@ -101,8 +101,10 @@ size_t gdn_chunk_workspace_bytes(int B, int T, int Hqk, int Hv, int K, int V,
  * The array is part of libgdn.so's device code object: every process that
  * loads the library holds those 32 MiB on every GPU it uses, until it ends,
  * whether or not it calls this entry point.
- * Problems whose gdn_chunk_workspace_bytes(...) exceeds 32 MiB (about 2200
- * tokens at 32 v-heads / 16 qk-heads, K = V = 128) are rejected with
+ * Problems whose gdn_chunk_workspace_bytes(...) exceeds 32 MiB (about 5,300
+ * tokens at 32 v-heads / 16 qk-heads, K = V = 128; about 2,300 with
+ * use_qk_l2norm, whose chain reads fp16 copies of the normalised q, k rows
+ * from the workspace) are rejected with
  * GDN_ERR_WORKSPACE before anything is enqueued.  Every call on one GPU
  * shares that GPU's scratch: calls that overlap on one GPU (different
  * streams, or host threads) race and must be serialised by the caller.
