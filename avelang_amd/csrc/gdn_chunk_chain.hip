@@ -579,7 +579,8 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
     // Tiles 2p and 2p + 1 go out as one 16-byte store per lane: lanes of
     // even grp keep row 16 (2p) + r16 and take the next 4 columns from their
     // partner (lane ^ 16), lanes of odd grp keep row 16 (2p + 1) + r16 and
-    // take the 4 columns before theirs (two stores per step instead of four)
+    // take the 4 columns before theirs (two stores per step instead of four;
+    // the exchange is a VALU row swap, no LDS)
     auto out_store = [&](const OutTile& ot, int j, bool live) {
       const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -591,12 +592,18 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         for (int p2 = 0; p2 < 2; ++p2) {
           const u32x2 mine0 = __builtin_bit_cast(u32x2, ot.v[sl][2 * p2]);
           const u32x2 mine1 = __builtin_bit_cast(u32x2, ot.v[sl][2 * p2 + 1]);
-          const u32x2 give = odd ? mine0 : mine1;
-          u32x2 got;
-          got[0] = __shfl_xor(give[0], 16);
-          got[1] = __shfl_xor(give[1], 16);
-          const u32x4 row = odd ? u32x4{got[0], got[1], mine1[0], mine1[1]}
-                                : u32x4{mine0[0], mine0[1], got[0], got[1]};
+          // v_permlane16_swap (vdst = mine0, src = mine1) trades rows 1, 3 of
+          // vdst with rows 0, 2 of src: vdst then holds, in an even grp, its
+          // own tile 2p and, in an odd grp, the partner's tile 2p+1; src the
+          // partner's tile 2p (even) or its own tile 2p+1 (odd) -- the row's
+          // first and second 4 columns in either case
+          u32x4 row;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(mine0[k], mine1[k], false, false);
+            row[k] = sw[0];
+            row[2 + k] = sw[1];
+          }
           __builtin_amdgcn_raw_buffer_store_b128(
               row, orsrc,
               (((16 * (2 * p2 + (odd ? 1 : 0)) + r16) * Hv + h) * V + 16 * (vt0 + sl) +
