@@ -72,7 +72,10 @@ extern "C" {
  * intermediates must stay inside fp16's range (|x| < 65504); l2-normalised
  * q / k (or use_qk_l2norm) and the v of a Qwen3-Next layer are orders of
  * magnitude inside it.  The final state is within ~4e-4 relative Frobenius
- * of the exact recurrence at any length.
+ * of the exact recurrence at any length.  Without use_qk_l2norm the output's
+ * q.S term is a bf16 MFMA product (q as given, the state rounded to bf16);
+ * with it an fp16 one (the normalised q as fp16); gdn_chunk_fwd_save gives
+ * the same o as gdn_chunk_fwd either way.
  */
 int gdn_chunk_fwd(const void* q, const void* k, const void* v,
                   const float* g, const float* beta,
