@@ -500,7 +500,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
       for (int i = 0; i < KB; ++i)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sh[i]), hr,
                                                ((16 * vt + rpi * i + lane / cpr) * K + 8 * c8) * 2,
-                                               0, 0);
+                                               0, kStoreStream);
       // deltas: lane t gathers token row t (its 16 columns) from the vnew
       // fragments in LDS -- element (t % 8) of fragment lane 16 ((t / 8) % 4)
       // + n of k-block t / 32 -- and stores it into the chunk's d block
@@ -522,9 +522,9 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         d1 = h2bf8(d1);
       }
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d0), dr,
-                                             ((2 * vt) * 64 + lane) * 16, 0, 0);
+                                             ((2 * vt) * 64 + lane) * 16, 0, kStoreStream);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, d1), dr,
-                                             ((2 * vt + 1) * 64 + lane) * 16, 0, 0);
+                                             ((2 * vt + 1) * 64 + lane) * 16, 0, kStoreStream);
       }
     };
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));

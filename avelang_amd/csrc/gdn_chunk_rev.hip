@@ -303,7 +303,7 @@ __global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
       for (int i = 0; i < KB; ++i)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, sh[i]), hr,
                                                ((16 * vt + rpi * i + lane / cpr) * K + 8 * c8) * 2,
-                                               0, 0);
+                                               0, kStoreStream);
       // lane t gathers token row t of dd from the fragments in LDS (element
       // t % 8 of fragment lane 16 ((t / 8) % 4) + n of k-block t / 32) and
       // stores it into the chunk's dd block ([V / 8 column groups][64 tokens]
@@ -323,9 +323,9 @@ __global__ __launch_bounds__(320) void chunk_rev_sw_kernel(
         }
       }
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d0), dr,
-                                             ((2 * vt) * 64 + lane) * 16, 0, 0);
+                                             ((2 * vt) * 64 + lane) * 16, 0, kStoreStream);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4l, d1), dr,
-                                             ((2 * vt + 1) * 64 + lane) * 16, 0, 0);
+                                             ((2 * vt + 1) * 64 + lane) * 16, 0, kStoreStream);
     };
     auto helper = [&](auto rolec) {
       constexpr int role = decltype(rolec)::value;

@@ -21,6 +21,11 @@ constexpr int kChunk = 64;  // tokens per chunk of the prefill path
 // Word 3 of a raw (stride 0) buffer resource on gfx950: out-of-range loads
 // return 0 and out-of-range stores are dropped.
 constexpr int kBufferFlags = 0x00020000;
+// Cache-policy operand of a buffer store for data no kernel of the same call
+// reads back soon (o, the training saves, the reverse chain's dS' / dd):
+// the nt (non-temporal, streaming) bit.  Whole 16-byte lanes only -- 2-byte
+// stores with it measured far slower.
+constexpr int kStoreStream = 2;
 constexpr int kWave = 64;   // CDNA wavefront width
 // s_waitcnt immediate (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
 // lgkmcnt 11:8) that waits for every vector-memory load and nothing else.
