@@ -207,13 +207,16 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int r16 = lane % 16, grp = lane / 16;
 
   // g and beta of the chunk's rows (wave 0), issued first so that their
-  // latency overlaps that of the K / Q rows rather than following it
+  // latency overlaps that of the K / Q rows rather than following it.  With
+  // the gating computed here (gate.a set) only its raw loads go out now; its
+  // math (gate_eval: the values gate_at gives) waits until the K / Q row
+  // loads are in flight too.
   float gv = 0.f, bv = 0.f;
+  GateRaw graw{};
   if (w == 0) {
     const size_t grow = (size_t)(t0 + min(lane, L - 1)) * Hv + h;
-    // gating computed here (gate.a set) or read from g / beta
     if (gate.a) {
-      gate_at(gate, (long long)grow, h, gv, bv);
+      graw = gate_load(gate, (long long)grow, h);
     } else {
       gv = g[grow];
       bv = beta[grow];
@@ -294,6 +297,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   // gates: wave 0 scans g over the 64 rows (padding rows add 0) and shares
   // G and beta through LDS
   if (w == 0) {
+    if (gate.a) gate_eval(gate, graw, gv, bv);
     gv = lane < L ? gv : 0.f;
     bv = lane < L ? bv : 0.f;
     gv = prefix_sum64(gv);
