@@ -67,8 +67,18 @@ namespace gdn {
 //   too, and the convert wave's registers would not fit beside two state
 //   waves.)  The output work is split over two waves as well (two o tiles
 //   each), since with one output wave that wave set the step.
+// Forms with o but no saves and one V tile per workgroup split the output work
+// over two waves (the role after the convert wave, or after the first output
+// wave without RAWK, is the second output wave).
+template <bool SAVE, bool OUT, int NS>
+constexpr bool chain_split_out() { return OUT && !SAVE && NS == 1; }
+template <bool SAVE, bool OUT, int NS, bool RAWK>
+constexpr int chain_waves() {
+  return NS + 2 + (SAVE && OUT ? 1 : 0) + (RAWK ? 1 : 0) + (chain_split_out<SAVE, OUT, NS>() ? 1 : 0);
+}
+
 template <int K, bool SAVE, bool OUT, int NS, bool RAWK, bool RAWQ>
-__global__ __launch_bounds__((NS + 2 + (SAVE && OUT ? 1 : 0) + (RAWK ? 2 : 0)) * 64) void
+__global__ __launch_bounds__((chain_waves<SAVE, OUT, NS, RAWK>() * 64)) void
 chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict__ qraw,
                       const uint16_t* __restrict__ kraw, const float* h0, float* ht,
                       uint16_t* __restrict__ o, const int32_t* __restrict__ cu, int N, int T,
@@ -394,13 +404,14 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
       step(j + 1, xb, xa);
     }
     if (j < nc) step(j, xa, xb);
-  } else if constexpr (RAWK) {
-    // ----------------------------------------------- output waves (RAWK) ----
+  } else if constexpr (chain_split_out<SAVE, OUT, NS>()) {
+    // ------------------------------------------- output waves (split) ----
     // Two output waves, each forming two of a chunk's four 16-row o tiles --
-    // tiles 0 and 3 (role NS + 1) and tiles 1 and 2 (role NS + 3), so that
+    // tiles 0 and 3 (role NS + 1) and tiles 1 and 2 (the last role), so that
     // each takes three P fragments and eleven MFMAs -- with the register
     // sets, step order and exact waits of the one-wave form below, over half
-    // its Q rows; the first also loads G and writes the gate factors.  Each
+    // its Q rows (the caller's bf16 rows with RAWQ, else the prep's fp16
+    // fragments); the first also loads G and writes the gate factors.  Each
     // wave's two tiles go out as one 16-byte store per lane.
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     auto run = [&](auto hfc) {
@@ -418,18 +429,32 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
       Regs rA, rB;
       auto load_qp = [&](Regs& r, int j) {
         const int ci = c_begin + j;
-        const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
-            kBufferFlags);
+        if constexpr (RAWQ) {
+          const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+          const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
+              kBufferFlags);
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const int ti = x ? T1 : T0;
+          for (int x = 0; x < 2; ++x) {
+            const int ti = x ? T1 : T0;
 #pragma unroll
-          for (int b = 0; b < KB; ++b)
-            r.qf[x][b] = __builtin_bit_cast(
-                u16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                           rq, ((16 * ti + r16) * Hqk * K + 32 * b + 8 * grp) * 2, 0, 0));
+            for (int b = 0; b < KB; ++b)
+              r.qf[x][b] = __builtin_bit_cast(
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                             rq, ((16 * ti + r16) * Hqk * K + 32 * b + 8 * grp) * 2, 0, 0));
+          }
+        } else {
+          const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+              ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            const int ti = x ? T1 : T0;
+#pragma unroll
+            for (int b = 0; b < KB; ++b)
+              r.qf[x][b] = __builtin_bit_cast(
+                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16,
+                                                               0, 0));
+          }
         }
         const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
             ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
@@ -463,7 +488,10 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         if (!live) return;
         u16x8 sh[KB];
 #pragma unroll
-        for (int b = 0; b < KB; ++b) sh[b] = h2bf8(Sx[b3][0][b][lane]);   // B of the bf16 Q S
+        for (int b = 0; b < KB; ++b) {
+          sh[b] = Sx[b3][0][b][lane];
+          if constexpr (RAWQ) sh[b] = h2bf8(sh[b]);   // B of the bf16 Q S
+        }
         const u16x8 vx0 = Vx[b3][0][0][lane], vx1 = Vx[b3][0][1][lane];
 #pragma unroll
         for (int x = 0; x < 2; ++x) {
@@ -471,8 +499,13 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
           f32x4 qa = zero4(), qb = zero4();
 #pragma unroll
           for (int b = 0; b < KB; b += 2) {
-            qa = mfma16(sh[b], r.qf[x][b], qa);
-            qb = mfma16(sh[b + 1], r.qf[x][b + 1], qb);
+            if constexpr (RAWQ) {
+              qa = mfma16(sh[b], r.qf[x][b], qa);
+              qb = mfma16(sh[b + 1], r.qf[x][b + 1], qb);
+            } else {
+              qa = mfma16h(sh[b], r.qf[x][b], qa);
+              qb = mfma16h(sh[b + 1], r.qf[x][b + 1], qb);
+            }
           }
           f32x4 pv = mfma16h(vx0, r.pf[x ? 1 : 0], zero4());
           if (x == 1) pv = mfma16h(vx1, r.pf[2], pv);   // T1 >= 2: k-block 1 too
@@ -539,7 +572,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         out_store(ov, nc - 1, true);
       }
     };
-    if (w == NS + 3) run(std::integral_constant<int, 1>{});
+    if (w == chain_waves<SAVE, OUT, NS, RAWK>() - 1) run(std::integral_constant<int, 1>{});
     else run(std::integral_constant<int, 0>{});
   } else {
     // ----------------------------------------------------- output wave ----
@@ -833,7 +866,6 @@ void launch_chain_sw(const uint16_t* v, const uint16_t* qraw, const uint16_t* kr
   // still has a state wave of its own (not with both outputs: a fifth wave
   // would halve the register budget; not with RAWK, see above)
   const long long chains = (long long)N * Hv * (V / 16);
-  constexpr int kExtra = SAVE && OUT ? 1 : 0;
   const bool rawq = OUT && qraw;
   const bool rawk = OUT && !SAVE && rawq && kraw;
   const bool two = !(SAVE && OUT) && !rawk && chain_two_tiles(N, Hv, V);
@@ -844,15 +876,22 @@ void launch_chain_sw(const uint16_t* v, const uint16_t* qraw, const uint16_t* kr
   };
   if constexpr (OUT) {
     if constexpr (!SAVE) {
-      if (rawk) return go(chunk_chain_sw_kernel<K, false, true, 1, true, true>, 5);
+      if (rawk) return go(chunk_chain_sw_kernel<K, false, true, 1, true, true>,
+                          chain_waves<false, true, 1, true>());
     }
     if (rawq) {
-      if (two) return go(chunk_chain_sw_kernel<K, SAVE, OUT, SAVE ? 1 : 2, false, true>, 4 + kExtra);
-      return go(chunk_chain_sw_kernel<K, SAVE, OUT, 1, false, true>, 3 + kExtra);
+      if (two)
+        return go(chunk_chain_sw_kernel<K, SAVE, OUT, SAVE ? 1 : 2, false, true>,
+                  chain_waves<SAVE, OUT, SAVE ? 1 : 2, false>());
+      return go(chunk_chain_sw_kernel<K, SAVE, OUT, 1, false, true>,
+                chain_waves<SAVE, OUT, 1, false>());
     }
   }
-  if (two) go(chunk_chain_sw_kernel<K, SAVE, OUT, (SAVE && OUT) ? 1 : 2, false, false>, 4 + kExtra);
-  else go(chunk_chain_sw_kernel<K, SAVE, OUT, 1, false, false>, 3 + kExtra);
+  if (two)
+    go(chunk_chain_sw_kernel<K, SAVE, OUT, (SAVE && OUT) ? 1 : 2, false, false>,
+       chain_waves<SAVE, OUT, (SAVE && OUT) ? 1 : 2, false>());
+  else
+    go(chunk_chain_sw_kernel<K, SAVE, OUT, 1, false, false>, chain_waves<SAVE, OUT, 1, false>());
 }
 
 #define GDN_CHAIN_INST(K_, SAVE_, OUT_)                                                     \
