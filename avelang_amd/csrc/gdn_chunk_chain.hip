@@ -67,11 +67,11 @@ namespace gdn {
 //   too, and the convert wave's registers would not fit beside two state
 //   waves.)  The output work is split over two waves as well (two o tiles
 //   each), since with one output wave that wave set the step.
-// Forms with o but no saves and one V tile per workgroup split the output work
-// over two waves (the role after the convert wave, or after the first output
-// wave without RAWK, is the second output wave).
+// Forms with o and one V tile per workgroup split the output work over two
+// waves (the last role is the second output wave; before it come the convert
+// wave with RAWK and the save wave with both outputs).
 template <bool SAVE, bool OUT, int NS>
-constexpr bool chain_split_out() { return OUT && !SAVE && NS == 1; }
+constexpr bool chain_split_out() { return OUT && NS == 1; }
 template <bool SAVE, bool OUT, int NS, bool RAWK>
 constexpr int chain_waves() {
   return NS + 2 + (SAVE && OUT ? 1 : 0) + (RAWK ? 1 : 0) + (chain_split_out<SAVE, OUT, NS>() ? 1 : 0);
@@ -404,176 +404,6 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
       step(j + 1, xb, xa);
     }
     if (j < nc) step(j, xa, xb);
-  } else if constexpr (chain_split_out<SAVE, OUT, NS>()) {
-    // ------------------------------------------- output waves (split) ----
-    // Two output waves, each forming two of a chunk's four 16-row o tiles --
-    // tiles 0 and 3 (role NS + 1) and tiles 1 and 2 (the last role), so that
-    // each takes three P fragments and eleven MFMAs -- with the register
-    // sets, step order and exact waits of the one-wave form below, over half
-    // its Q rows (the caller's bf16 rows with RAWQ, else the prep's fp16
-    // fragments); the first also loads G and writes the gate factors.  Each
-    // wave's two tiles go out as one 16-byte store per lane.
-    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-    auto run = [&](auto hfc) {
-      constexpr int HF = decltype(hfc)::value;
-      constexpr int T0 = HF ? 1 : 0, T1 = HF ? 2 : 3;
-      constexpr int kQP = 2 * KB + 3;    // Q rows of two tiles, three P fragments
-      constexpr int kVG = HF ? 0 : 1;    // G
-      constexpr int kStores = 1;
-      constexpr int kWait = (kStores + kQP + kVG) + kStores;
-      struct Regs {
-        u16x8 qf[2][KB];   // Q rows 16 T + r16 (T = T0, T1), B operand of (Q S)^T
-        u16x8 pf[3];       // P fragments tb_slot(T0, 0), tb_slot(T1, 0), tb_slot(T1, 1)
-        float G;
-      };
-      Regs rA, rB;
-      auto load_qp = [&](Regs& r, int j) {
-        const int ci = c_begin + j;
-        if constexpr (RAWQ) {
-          const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-          const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-              const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
-              kBufferFlags);
-#pragma unroll
-          for (int x = 0; x < 2; ++x) {
-            const int ti = x ? T1 : T0;
-#pragma unroll
-            for (int b = 0; b < KB; ++b)
-              r.qf[x][b] = __builtin_bit_cast(
-                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                             rq, ((16 * ti + r16) * Hqk * K + 32 * b + 8 * grp) * 2, 0, 0));
-          }
-        } else {
-          const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-              ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
-#pragma unroll
-          for (int x = 0; x < 2; ++x) {
-            const int ti = x ? T1 : T0;
-#pragma unroll
-            for (int b = 0; b < KB; ++b)
-              r.qf[x][b] = __builtin_bit_cast(
-                  u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16,
-                                                               0, 0));
-          }
-        }
-        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-            ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
-        constexpr int slot[3] = {tb_slot(T0, 0), tb_slot(T1, 0), tb_slot(T1, 1)};
-#pragma unroll
-        for (int i = 0; i < 3; ++i)
-          r.pf[i] = __builtin_bit_cast(
-              u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (slot[i] * 64 + lane) * 16, 0, 0));
-      };
-      auto load_vg = [&](Regs& r, int j) {
-        const int ci = c_begin + j;
-        const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(ws.gate + ((size_t)ci * Hv + h) * 64), 0, 256, kBufferFlags);
-        r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
-      };
-      auto write_vg = [&](const Regs& r, int j) {
-        const int buf = j % 3;
-        const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-        const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
-        const float eg = __expf(r.G);
-        Gst[buf][0][lane] = eg;
-        Gst[buf][1][lane] = __expf(GL - r.G);
-        if (lane == L - 1) Egl[buf] = eg;
-      };
-      // o^T tiles T0, T1 of chunk j (lane (r16, grp): token row 16 T + r16,
-      // columns 16 vt0 + 4 grp .. + 3)
-      auto out_form = [&](const Regs& r, int j, bool live, u16x4 (&ov)[2]) {
-        const int b3 = j % 3;
-        ov[0] = u16x4{0, 0, 0, 0};
-        ov[1] = ov[0];
-        if (!live) return;
-        u16x8 sh[KB];
-#pragma unroll
-        for (int b = 0; b < KB; ++b) {
-          sh[b] = Sx[b3][0][b][lane];
-          if constexpr (RAWQ) sh[b] = h2bf8(sh[b]);   // B of the bf16 Q S
-        }
-        const u16x8 vx0 = Vx[b3][0][0][lane], vx1 = Vx[b3][0][1][lane];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const int ti = x ? T1 : T0;
-          f32x4 qa = zero4(), qb = zero4();
-#pragma unroll
-          for (int b = 0; b < KB; b += 2) {
-            if constexpr (RAWQ) {
-              qa = mfma16(sh[b], r.qf[x][b], qa);
-              qb = mfma16(sh[b + 1], r.qf[x][b + 1], qb);
-            } else {
-              qa = mfma16h(sh[b], r.qf[x][b], qa);
-              qb = mfma16h(sh[b + 1], r.qf[x][b + 1], qb);
-            }
-          }
-          f32x4 pv = mfma16h(vx0, r.pf[x ? 1 : 0], zero4());
-          if (x == 1) pv = mfma16h(vx1, r.pf[2], pv);   // T1 >= 2: k-block 1 too
-          const float egi = Gst[b3][0][16 * ti + r16];
-          ov[x] = f2bf4((scale * egi) * (qa + qb) + pv);
-        }
-      };
-      // v_permlane16_swap (vdst = tile T0, src = tile T1) trades rows 1, 3 of
-      // vdst with rows 0, 2 of src: a lane of even grp then holds columns
-      // 4 grp .. + 7 of tile T0's row, a lane of odd grp columns 4 (grp - 1)
-      // .. + 7 of tile T1's row
-      auto out_store = [&](const u16x4 (&ov)[2], int j, bool live) {
-        const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
-        const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-            o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-        const u32x2 m0 = __builtin_bit_cast(u32x2, ov[0]);
-        const u32x2 m1 = __builtin_bit_cast(u32x2, ov[1]);
-        u32x4 row;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const auto sw = __builtin_amdgcn_permlane16_swap(m0[k], m1[k], false, false);
-          row[k] = sw[0];
-          row[2 + k] = sw[1];
-        }
-        __builtin_amdgcn_raw_buffer_store_b128(
-            row, orsrc,
-            (((16 * ((grp & 1) ? T1 : T0) + r16) * Hv + h) * V + 16 * vt0 + 4 * (grp & 2)) * 2,
-            0, 0);
-      };
-      u16x4 ov[2] = {u16x4{0, 0, 0, 0}, u16x4{0, 0, 0, 0}};
-      if (nc > 0) {
-        if constexpr (HF == 0) {
-          load_vg(rA, 0);
-          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-          write_vg(rA, 0);
-          load_vg(rB, min(1, nc - 1));
-        }
-        out_store(ov, 0, false);
-        load_qp(rA, 0);
-        if constexpr (HF == 0) load_vg(rA, min(2, nc - 1));
-        out_store(ov, 0, false);
-      }
-      __syncthreads();
-      auto step = [&](int j, Regs& r) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWait));   // chunk j-1's Q / P, chunk j+1's G
-        if constexpr (HF == 0) {
-          if (j + 1 < nc) write_vg(r, j + 1);
-        }
-        out_form(r, j - 1, j >= 1, ov);
-        load_qp(r, min(j + 1, nc - 1));
-        if constexpr (HF == 0) load_vg(r, min(j + 3, nc - 1));
-        out_store(ov, j - 1, j >= 1);
-        __syncthreads();
-      };
-      int j = 0;
-      for (; j + 1 < nc; j += 2) {
-        step(j, rB);
-        step(j + 1, rA);
-      }
-      if (j < nc) step(j, rB);
-      if (nc > 0) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        out_form((nc - 1) & 1 ? rB : rA, nc - 1, true, ov);
-        out_store(ov, nc - 1, true);
-      }
-    };
-    if (w == chain_waves<SAVE, OUT, NS, RAWK>() - 1) run(std::integral_constant<int, 1>{});
-    else run(std::integral_constant<int, 0>{});
   } else {
     // ----------------------------------------------------- output wave ----
     // During step j: writes chunk j+1's gate factors into stage buffer
@@ -801,6 +631,178 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         __syncthreads();
       }
       if (nc > 0) save_chunk(nc - 1, true);
+      return;
+    }
+    if constexpr (chain_split_out<SAVE, OUT, NS>()) {
+      // ------------------------------------------- output waves (split) ----
+      // Two output waves, each forming two of a chunk's four 16-row o tiles --
+      // tiles 0 and 3 (role NS + 1) and tiles 1 and 2 (the last role), so that
+      // each takes three P fragments and eleven MFMAs -- with the register
+      // sets, step order and exact waits of the one-wave form below, over half
+      // its Q rows (the caller's bf16 rows with RAWQ, else the prep's fp16
+      // fragments); the first also loads G and writes the gate factors.  Each
+      // wave's two tiles go out as one 16-byte store per lane.
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      auto run = [&](auto hfc) {
+        constexpr int HF = decltype(hfc)::value;
+        constexpr int T0 = HF ? 1 : 0, T1 = HF ? 2 : 3;
+        constexpr int kQP = 2 * KB + 3;    // Q rows of two tiles, three P fragments
+        constexpr int kVG = HF ? 0 : 1;    // G
+        constexpr int kStores = 1;
+        constexpr int kWait = (kStores + kQP + kVG) + kStores;
+        struct Regs {
+          u16x8 qf[2][KB];   // Q rows 16 T + r16 (T = T0, T1), B operand of (Q S)^T
+          u16x8 pf[3];       // P fragments tb_slot(T0, 0), tb_slot(T1, 0), tb_slot(T1, 1)
+          float G;
+        };
+        Regs rA, rB;
+        auto load_qp = [&](Regs& r, int j) {
+          const int ci = c_begin + j;
+          if constexpr (RAWQ) {
+            const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+            const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
+                kBufferFlags);
+  #pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              const int ti = x ? T1 : T0;
+  #pragma unroll
+              for (int b = 0; b < KB; ++b)
+                r.qf[x][b] = __builtin_bit_cast(
+                    u16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                               rq, ((16 * ti + r16) * Hqk * K + 32 * b + 8 * grp) * 2, 0, 0));
+            }
+          } else {
+            const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+                ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
+  #pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              const int ti = x ? T1 : T0;
+  #pragma unroll
+              for (int b = 0; b < KB; ++b)
+                r.qf[x][b] = __builtin_bit_cast(
+                    u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16,
+                                                                 0, 0));
+            }
+          }
+          const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+              ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
+          constexpr int slot[3] = {tb_slot(T0, 0), tb_slot(T1, 0), tb_slot(T1, 1)};
+  #pragma unroll
+          for (int i = 0; i < 3; ++i)
+            r.pf[i] = __builtin_bit_cast(
+                u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (slot[i] * 64 + lane) * 16, 0, 0));
+        };
+        auto load_vg = [&](Regs& r, int j) {
+          const int ci = c_begin + j;
+          const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<float*>(ws.gate + ((size_t)ci * Hv + h) * 64), 0, 256, kBufferFlags);
+          r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
+        };
+        auto write_vg = [&](const Regs& r, int j) {
+          const int buf = j % 3;
+          const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+          const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
+          const float eg = __expf(r.G);
+          Gst[buf][0][lane] = eg;
+          Gst[buf][1][lane] = __expf(GL - r.G);
+          if (lane == L - 1) Egl[buf] = eg;
+        };
+        // o^T tiles T0, T1 of chunk j (lane (r16, grp): token row 16 T + r16,
+        // columns 16 vt0 + 4 grp .. + 3)
+        auto out_form = [&](const Regs& r, int j, bool live, u16x4 (&ov)[2]) {
+          const int b3 = j % 3;
+          ov[0] = u16x4{0, 0, 0, 0};
+          ov[1] = ov[0];
+          if (!live) return;
+          u16x8 sh[KB];
+  #pragma unroll
+          for (int b = 0; b < KB; ++b) {
+            sh[b] = Sx[b3][0][b][lane];
+            if constexpr (RAWQ) sh[b] = h2bf8(sh[b]);   // B of the bf16 Q S
+          }
+          const u16x8 vx0 = Vx[b3][0][0][lane], vx1 = Vx[b3][0][1][lane];
+  #pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            const int ti = x ? T1 : T0;
+            f32x4 qa = zero4(), qb = zero4();
+  #pragma unroll
+            for (int b = 0; b < KB; b += 2) {
+              if constexpr (RAWQ) {
+                qa = mfma16(sh[b], r.qf[x][b], qa);
+                qb = mfma16(sh[b + 1], r.qf[x][b + 1], qb);
+              } else {
+                qa = mfma16h(sh[b], r.qf[x][b], qa);
+                qb = mfma16h(sh[b + 1], r.qf[x][b + 1], qb);
+              }
+            }
+            f32x4 pv = mfma16h(vx0, r.pf[x ? 1 : 0], zero4());
+            if (x == 1) pv = mfma16h(vx1, r.pf[2], pv);   // T1 >= 2: k-block 1 too
+            const float egi = Gst[b3][0][16 * ti + r16];
+            ov[x] = f2bf4((scale * egi) * (qa + qb) + pv);
+          }
+        };
+        // v_permlane16_swap (vdst = tile T0, src = tile T1) trades rows 1, 3 of
+        // vdst with rows 0, 2 of src: a lane of even grp then holds columns
+        // 4 grp .. + 7 of tile T0's row, a lane of odd grp columns 4 (grp - 1)
+        // .. + 7 of tile T1's row
+        auto out_store = [&](const u16x4 (&ov)[2], int j, bool live) {
+          const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
+          const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+              o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
+          const u32x2 m0 = __builtin_bit_cast(u32x2, ov[0]);
+          const u32x2 m1 = __builtin_bit_cast(u32x2, ov[1]);
+          u32x4 row;
+  #pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(m0[k], m1[k], false, false);
+            row[k] = sw[0];
+            row[2 + k] = sw[1];
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(
+              row, orsrc,
+              (((16 * ((grp & 1) ? T1 : T0) + r16) * Hv + h) * V + 16 * vt0 + 4 * (grp & 2)) * 2,
+              0, 0);
+        };
+        u16x4 ov[2] = {u16x4{0, 0, 0, 0}, u16x4{0, 0, 0, 0}};
+        if (nc > 0) {
+          if constexpr (HF == 0) {
+            load_vg(rA, 0);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            write_vg(rA, 0);
+            load_vg(rB, min(1, nc - 1));
+          }
+          out_store(ov, 0, false);
+          load_qp(rA, 0);
+          if constexpr (HF == 0) load_vg(rA, min(2, nc - 1));
+          out_store(ov, 0, false);
+        }
+        __syncthreads();
+        auto step = [&](int j, Regs& r) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWait));   // chunk j-1's Q / P, chunk j+1's G
+          if constexpr (HF == 0) {
+            if (j + 1 < nc) write_vg(r, j + 1);
+          }
+          out_form(r, j - 1, j >= 1, ov);
+          load_qp(r, min(j + 1, nc - 1));
+          if constexpr (HF == 0) load_vg(r, min(j + 3, nc - 1));
+          out_store(ov, j - 1, j >= 1);
+          __syncthreads();
+        };
+        int j = 0;
+        for (; j + 1 < nc; j += 2) {
+          step(j, rB);
+          step(j + 1, rA);
+        }
+        if (j < nc) step(j, rB);
+        if (nc > 0) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+          out_form((nc - 1) & 1 ? rB : rA, nc - 1, true, ov);
+          out_store(ov, nc - 1, true);
+        }
+      };
+      if (w == chain_waves<SAVE, OUT, NS, RAWK>() - 1) run(std::integral_constant<int, 1>{});
+      else run(std::integral_constant<int, 0>{});
       return;
     }
     // Every step issues its loads, then its stores (the o tiles, or without
