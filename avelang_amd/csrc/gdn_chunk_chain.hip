@@ -67,11 +67,11 @@ namespace gdn {
 //   too, and the convert wave's registers would not fit beside two state
 //   waves.)  The output work is split over two waves as well (two o tiles
 //   each), since with one output wave that wave set the step.
-// Forms with o and one V tile per workgroup split the output work over two
-// waves (the last role is the second output wave; before it come the convert
-// wave with RAWK and the save wave with both outputs).
+// Forms with o split the output work over two waves (the last role is the
+// second output wave; before it come the convert wave with RAWK and the save
+// wave with both outputs).
 template <bool SAVE, bool OUT, int NS>
-constexpr bool chain_split_out() { return OUT && NS == 1; }
+constexpr bool chain_split_out() { return OUT && (NS == 1 || !SAVE); }
 template <bool SAVE, bool OUT, int NS, bool RAWK>
 constexpr int chain_waves() {
   return NS + 2 + (SAVE && OUT ? 1 : 0) + (RAWK ? 1 : 0) + (chain_split_out<SAVE, OUT, NS>() ? 1 : 0);
@@ -648,7 +648,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         constexpr int T0 = HF ? 1 : 0, T1 = HF ? 2 : 3;
         constexpr int kQP = 2 * KB + 3;    // Q rows of two tiles, three P fragments
         constexpr int kVG = HF ? 0 : 1;    // G
-        constexpr int kStores = 1;
+        constexpr int kStores = NS;   // one o store per V tile
         constexpr int kWait = (kStores + kQP + kVG) + kStores;
         struct Regs {
           u16x8 qf[2][KB];   // Q rows 16 T + r16 (T = T0, T1), B operand of (Q S)^T
@@ -663,10 +663,10 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
             const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
                 kBufferFlags);
-  #pragma unroll
+#pragma unroll
             for (int x = 0; x < 2; ++x) {
               const int ti = x ? T1 : T0;
-  #pragma unroll
+#pragma unroll
               for (int b = 0; b < KB; ++b)
                 r.qf[x][b] = __builtin_bit_cast(
                     u16x8, __builtin_amdgcn_raw_buffer_load_b128(
@@ -675,10 +675,10 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
           } else {
             const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
                 ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
-  #pragma unroll
+#pragma unroll
             for (int x = 0; x < 2; ++x) {
               const int ti = x ? T1 : T0;
-  #pragma unroll
+#pragma unroll
               for (int b = 0; b < KB; ++b)
                 r.qf[x][b] = __builtin_bit_cast(
                     u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16,
@@ -688,7 +688,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
           const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
               ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
           constexpr int slot[3] = {tb_slot(T0, 0), tb_slot(T1, 0), tb_slot(T1, 1)};
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 3; ++i)
             r.pf[i] = __builtin_bit_cast(
                 u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (slot[i] * 64 + lane) * 16, 0, 0));
@@ -710,61 +710,70 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         };
         // o^T tiles T0, T1 of chunk j (lane (r16, grp): token row 16 T + r16,
         // columns 16 vt0 + 4 grp .. + 3)
-        auto out_form = [&](const Regs& r, int j, bool live, u16x4 (&ov)[2]) {
+        auto out_form = [&](const Regs& r, int j, bool live, u16x4 (&ov)[NS][2]) {
           const int b3 = j % 3;
-          ov[0] = u16x4{0, 0, 0, 0};
-          ov[1] = ov[0];
+#pragma unroll
+          for (int sl = 0; sl < NS; ++sl) ov[sl][0] = ov[sl][1] = u16x4{0, 0, 0, 0};
           if (!live) return;
-          u16x8 sh[KB];
-  #pragma unroll
-          for (int b = 0; b < KB; ++b) {
-            sh[b] = Sx[b3][0][b][lane];
-            if constexpr (RAWQ) sh[b] = h2bf8(sh[b]);   // B of the bf16 Q S
-          }
-          const u16x8 vx0 = Vx[b3][0][0][lane], vx1 = Vx[b3][0][1][lane];
-  #pragma unroll
-          for (int x = 0; x < 2; ++x) {
-            const int ti = x ? T1 : T0;
-            f32x4 qa = zero4(), qb = zero4();
-  #pragma unroll
-            for (int b = 0; b < KB; b += 2) {
-              if constexpr (RAWQ) {
-                qa = mfma16(sh[b], r.qf[x][b], qa);
-                qb = mfma16(sh[b + 1], r.qf[x][b + 1], qb);
-              } else {
-                qa = mfma16h(sh[b], r.qf[x][b], qa);
-                qb = mfma16h(sh[b + 1], r.qf[x][b + 1], qb);
-              }
+#pragma unroll
+          for (int sl = 0; sl < NS; ++sl) {
+            u16x8 sh[KB];
+#pragma unroll
+            for (int b = 0; b < KB; ++b) {
+              sh[b] = Sx[b3][sl][b][lane];
+              if constexpr (RAWQ) sh[b] = h2bf8(sh[b]);   // B of the bf16 Q S
             }
-            f32x4 pv = mfma16h(vx0, r.pf[x ? 1 : 0], zero4());
-            if (x == 1) pv = mfma16h(vx1, r.pf[2], pv);   // T1 >= 2: k-block 1 too
-            const float egi = Gst[b3][0][16 * ti + r16];
-            ov[x] = f2bf4((scale * egi) * (qa + qb) + pv);
+            const u16x8 vx0 = Vx[b3][sl][0][lane], vx1 = Vx[b3][sl][1][lane];
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              const int ti = x ? T1 : T0;
+              f32x4 qa = zero4(), qb = zero4();
+#pragma unroll
+              for (int b = 0; b < KB; b += 2) {
+                if constexpr (RAWQ) {
+                  qa = mfma16(sh[b], r.qf[x][b], qa);
+                  qb = mfma16(sh[b + 1], r.qf[x][b + 1], qb);
+                } else {
+                  qa = mfma16h(sh[b], r.qf[x][b], qa);
+                  qb = mfma16h(sh[b + 1], r.qf[x][b + 1], qb);
+                }
+              }
+              f32x4 pv = mfma16h(vx0, r.pf[x ? 1 : 0], zero4());
+              if (x == 1) pv = mfma16h(vx1, r.pf[2], pv);   // T1 >= 2: k-block 1 too
+              const float egi = Gst[b3][0][16 * ti + r16];
+              ov[sl][x] = f2bf4((scale * egi) * (qa + qb) + pv);
+            }
           }
         };
         // v_permlane16_swap (vdst = tile T0, src = tile T1) trades rows 1, 3 of
         // vdst with rows 0, 2 of src: a lane of even grp then holds columns
         // 4 grp .. + 7 of tile T0's row, a lane of odd grp columns 4 (grp - 1)
-        // .. + 7 of tile T1's row
-        auto out_store = [&](const u16x4 (&ov)[2], int j, bool live) {
+        // .. + 7 of tile T1's row; one store per V tile
+        auto out_store = [&](const u16x4 (&ov)[NS][2], int j, bool live) {
           const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
           const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
               o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-          const u32x2 m0 = __builtin_bit_cast(u32x2, ov[0]);
-          const u32x2 m1 = __builtin_bit_cast(u32x2, ov[1]);
-          u32x4 row;
-  #pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const auto sw = __builtin_amdgcn_permlane16_swap(m0[k], m1[k], false, false);
-            row[k] = sw[0];
-            row[2 + k] = sw[1];
+#pragma unroll
+          for (int sl = 0; sl < NS; ++sl) {
+            const u32x2 m0 = __builtin_bit_cast(u32x2, ov[sl][0]);
+            const u32x2 m1 = __builtin_bit_cast(u32x2, ov[sl][1]);
+            u32x4 row;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const auto sw = __builtin_amdgcn_permlane16_swap(m0[k], m1[k], false, false);
+              row[k] = sw[0];
+              row[2 + k] = sw[1];
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(
+                row, orsrc,
+                (((16 * ((grp & 1) ? T1 : T0) + r16) * Hv + h) * V + 16 * (vt0 + sl) +
+                 4 * (grp & 2)) * 2,
+                0, 0);
           }
-          __builtin_amdgcn_raw_buffer_store_b128(
-              row, orsrc,
-              (((16 * ((grp & 1) ? T1 : T0) + r16) * Hv + h) * V + 16 * vt0 + 4 * (grp & 2)) * 2,
-              0, 0);
         };
-        u16x4 ov[2] = {u16x4{0, 0, 0, 0}, u16x4{0, 0, 0, 0}};
+        u16x4 ov[NS][2];
+#pragma unroll
+        for (int sl = 0; sl < NS; ++sl) ov[sl][0] = ov[sl][1] = u16x4{0, 0, 0, 0};
         if (nc > 0) {
           if constexpr (HF == 0) {
             load_vg(rA, 0);
