@@ -20,11 +20,12 @@
 //   order) and V tiles straight into LDS (buffer_load ... lds) while step c
 //   runs.
 //
-//   the output wave writes chunk c+1's gate factors into LDS and forms chunk
-//   c-1's output
-//   from the state and vnew fragments the state waves leave in LDS:
+//   two output waves form chunk c-1's output, two of its four 16-row tiles
+//   each, from the state and vnew fragments the state waves leave in LDS:
 //       o = scale e^G (Q S) + P vnew
-//   (with both the backward's saves and o, a save wave stores the former).
+//   and the first writes chunk c+1's gate factors into LDS (with both the
+//   backward's saves and o, a save wave stores the former; without o, one
+//   wave writes the gate factors and stores the saves).
 //
 // One s_barrier per chunk step hands the buffers over (three stage buffers,
 // three output buffers).  The state wave issues no global load at all.
@@ -48,12 +49,12 @@ namespace gdn {
 // ht.  Forward <K, false, true>, the backward's recomputation <K, true,
 // false>, a training forward <K, true, true>.  NS: V tiles (slices) per
 // workgroup, one state wave each, sharing the stage wave's K / Tb buffers
-// and the output wave's Q / P (2 when there are enough chains to fill the
+// and the output waves' Q / P (2 when there are enough chains to fill the
 // GPU twice over).
 //
 // Without use_qk_l2norm the chain reads the caller's bf16 rows where the
 // prep kernel would otherwise have to copy them:
-// RAWQ (forms with OUT): the output wave takes Q S on bf16 MFMA, Q rows
+// RAWQ (forms with OUT): the output waves take Q S on bf16 MFMA, Q rows
 //   loaded as they are and the state's fp16 fragments re-rounded to bf16 --
 //   the rounding the operator's bf16 contract allows there, while the state's
 //   own products keep fp16 (the prep writes no fp16 Q copy).  The state wave
@@ -85,6 +86,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
                       int total, int Hqk, int Hv, int V, float scale, ChunkWs ws) {
   static_assert(!RAWK || (OUT && !SAVE && NS == 1 && RAWQ), "RAWK is a plain forward");
   static_assert(!RAWQ || OUT, "RAWQ forms o");
+  static_assert(!OUT || chain_split_out<SAVE, OUT, NS>(), "every form with o splits its output");
   constexpr int KB = K / 32;   // k-blocks over the key index
   constexpr int ST = K / 16;   // 16-row state tiles
   // Stage buffers (chunk c in buffer c % 3): the chunk's K rows (KLayout),
@@ -98,7 +100,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
   __shared__ __attribute__((aligned(16))) float Gst[3][2][64];
   __shared__ float Egl[3];
   // Output buffers (chunk c in buffer c % 3), left by the state wave for
-  // the output wave: the state's hi B fragments at the chunk start and
+  // the output waves: the state's hi B fragments at the chunk start and
   // vnew (bf16) as B fragments.
   __shared__ __attribute__((aligned(16))) u16x8 Sx[3][NS][KB][64];
   __shared__ __attribute__((aligned(16))) u16x8 Vx[3][NS][2][64];
@@ -248,7 +250,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
         for (int ti = 2; ti < 4; ++ti) vn[ti] = mfma16h(ta[tb_slot(ti, 1)], y1, vn[ti]);
       }
       // U = e^(G_last - G) vnew and vnew itself (both fp16, the latter for
-      // the output wave); S = e^G_last S + K^T U, k-block by k-block
+      // the output waves); S = e^G_last S + K^T U, k-block by k-block
 #pragma unroll
       for (int t = 0; t < ST; ++t) S[t] = S[t] * egl;
 #pragma unroll
@@ -405,84 +407,12 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
     }
     if (j < nc) step(j, xa, xb);
   } else {
-    // ----------------------------------------------------- output wave ----
-    // During step j: writes chunk j+1's gate factors into stage buffer
-    // (j+1) % 3, forms chunk j-1's output, then loads chunk j+1's Q and P
-    // fragments and chunk j+3's G into registers.  A register set is loaded two
-    // steps before it is used (two sets, the loop unrolled by two), and
-    // every step issues the same loads and stores, so each wait names an
-    // exact count.
-    constexpr int kQP = OUT ? 4 * KB + 6 : 0;   // Q / P loads per chunk
-    constexpr int kVG = 1;                      // G
-    // with both outputs, the saves go to a wave of their own (the last)
+    // ------------------------------------------------ output / save waves ----
+    // Forms with o: two output waves (below) and, with the saves too, a save
+    // wave.  Forms without o (the backward's recomputation): one wave that
+    // writes the gate factors and stores the saves.
+    // with both outputs, the saves go to a wave of their own
     constexpr bool kSplit = SAVE && OUT;
-    constexpr int kSave = SAVE && !kSplit ? NS * (KB + 2) : 0;   // state and delta stores per chunk
-    constexpr int kStep = (OUT ? 2 * NS : 0) + kSave + kQP + kVG;   // stores + loads per step
-    // The stores of a step (o tiles, or the saves) go after its loads, and
-    // the step's wait lets the previous step's stores stay in flight as well
-    // (the counter retires loads and stores in issue order): the stores then
-    // have two steps to drain instead of one
-    constexpr int kStores = (OUT ? 2 * NS : 0) + kSave;
-    constexpr int kWait = kStep + kStores;
-    struct Regs {
-      u16x8 qf[4][KB];   // Q rows 16 ti + r16, B operand of (Q S)^T
-      u16x8 pf[6];       // P fragments by tb_slot
-      float G;           // G of token `lane`
-    };
-    Regs rA, rB;
-    // the chunk's Q fragments (the prep kernel's fp16 copy) and P fragments,
-    // both contiguous 1 KiB blocks
-    auto load_qp = [&](Regs& r, int j) {
-      if constexpr (!OUT) return;
-      const int ci = c_begin + j;
-      if constexpr (RAWQ) {
-        // bf16 B fragments straight from q: row 16 ti + r16 of the chunk,
-        // columns 32 b + 8 grp .. + 7 (rows past the sequence end read as 0)
-        const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(qraw + ((size_t)t0 * Hqk + hq) * K), 0, L * Hqk * K * 2,
-            kBufferFlags);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-          for (int b = 0; b < KB; ++b)
-            r.qf[ti][b] = __builtin_bit_cast(
-                u16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                           rq, ((16 * ti + r16) * Hqk * K + 32 * b + 8 * grp) * 2, 0, 0));
-        }
-      } else {
-        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-            ws.q16 + ((size_t)ci * Hqk + hq) * 4 * KB * 64, 0, 4 * KB * 64 * 16, kBufferFlags);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-#pragma unroll
-          for (int b = 0; b < KB; ++b)
-            r.qf[ti][b] = __builtin_bit_cast(
-                u16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, ((ti * KB + b) * 64 + lane) * 16, 0, 0));
-        }
-      }
-      const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-          ws.pfrag + ((size_t)ci * Hv + h) * 6 * 64, 0, 6 * 64 * 16, kBufferFlags);
-#pragma unroll
-      for (int i = 0; i < 6; ++i)
-        r.pf[i] = __builtin_bit_cast(
-            u16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, (i * 64 + lane) * 16, 0, 0));
-    };
-    auto load_vg = [&](Regs& r, int j) {
-      const int ci = c_begin + j;
-      const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<float*>(ws.gate + ((size_t)ci * Hv + h) * 64), 0, 256, kBufferFlags);
-      r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
-    };
-    auto write_vg = [&](const Regs& r, int j) {
-      const int buf = j % 3;
-      const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
-      const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
-      const float eg = __expf(r.G);
-      Gst[buf][0][lane] = eg;
-      Gst[buf][1][lane] = __expf(GL - r.G);
-      if (lane == L - 1) Egl[buf] = eg;
-    };
     // SAVE: the chunk's start state (hs[chunk][v-head] = S^T, [V][K], the
     // hi fragments) and its deltas (dl, token-major); live = false stores
     // to empty resources (dropped)
@@ -538,91 +468,6 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
                                              ((2 * vt + 1) * 64 + lane) * 16, 0, kStoreStream);
       }
     };
-    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-    // o^T tiles of chunk j: lane (r16, grp) holds token row 16 ti + r16,
-    // columns 16 vt + 4 grp .. + 3 (one 8-byte store per tile).  Formed
-    // from register set r before the step's loads overwrite it, stored after
-    // them (stores retire in issue order with the loads, so a store issued
-    // ahead of the step's loads would hold up the next step's wait).  With
-    // live = false (no chunk yet) every store goes to an empty resource and
-    // is dropped.
-    struct OutTile {
-      u16x4 v[NS][4];
-    };
-    auto out_form = [&](const Regs& r, int j, bool live, OutTile& ot) {
-      const int b3 = j % 3;
-#pragma unroll
-      for (int sl = 0; sl < NS; ++sl) {
-        u16x8 sh[KB], vx[2];
-        if (live) {
-#pragma unroll
-          for (int b = 0; b < KB; ++b) {
-            sh[b] = Sx[b3][sl][b][lane];
-            if constexpr (RAWQ) sh[b] = h2bf8(sh[b]);   // B of the bf16 Q S
-          }
-          vx[0] = Vx[b3][sl][0][lane];
-          vx[1] = Vx[b3][sl][1][lane];
-        }
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-          u16x4 ov = {0, 0, 0, 0};
-          if (live) {
-            f32x4 qa = zero4(), qb = zero4();
-#pragma unroll
-            for (int b = 0; b < KB; b += 2) {
-              if constexpr (RAWQ) {
-                qa = mfma16(sh[b], r.qf[ti][b], qa);
-                qb = mfma16(sh[b + 1], r.qf[ti][b + 1], qb);
-              } else {
-                qa = mfma16h(sh[b], r.qf[ti][b], qa);
-                qb = mfma16h(sh[b + 1], r.qf[ti][b + 1], qb);
-              }
-            }
-            f32x4 pv = mfma16h(vx[0], r.pf[tb_slot(ti, 0)], zero4());
-            if (ti >= 2) pv = mfma16h(vx[1], r.pf[tb_slot(ti, 1)], pv);
-            const float egi = Gst[b3][0][16 * ti + r16];
-            ov = f2bf4((scale * egi) * (qa + qb) + pv);
-          }
-          ot.v[sl][ti] = ov;
-        }
-      }
-    };
-    // Tiles 2p and 2p + 1 go out as one 16-byte store per lane: lanes of
-    // even grp keep row 16 (2p) + r16 and take the next 4 columns from their
-    // partner (lane ^ 16), lanes of odd grp keep row 16 (2p + 1) + r16 and
-    // take the 4 columns before theirs (two stores per step instead of four;
-    // the exchange is a VALU row swap, no LDS)
-    auto out_store = [&](const OutTile& ot, int j, bool live) {
-      const int t0 = s + j * kChunk, L = live ? min(kChunk, e - t0) : 0;
-      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-          o + (size_t)(live ? t0 : 0) * Hv * V, 0, L * Hv * V * 2, kBufferFlags);
-      const bool odd = grp & 1;
-#pragma unroll
-      for (int sl = 0; sl < NS; ++sl) {
-#pragma unroll
-        for (int p2 = 0; p2 < 2; ++p2) {
-          const u32x2 mine0 = __builtin_bit_cast(u32x2, ot.v[sl][2 * p2]);
-          const u32x2 mine1 = __builtin_bit_cast(u32x2, ot.v[sl][2 * p2 + 1]);
-          // v_permlane16_swap (vdst = mine0, src = mine1) trades rows 1, 3 of
-          // vdst with rows 0, 2 of src: vdst then holds, in an even grp, its
-          // own tile 2p and, in an odd grp, the partner's tile 2p+1; src the
-          // partner's tile 2p (even) or its own tile 2p+1 (odd) -- the row's
-          // first and second 4 columns in either case
-          u32x4 row;
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const auto sw = __builtin_amdgcn_permlane16_swap(mine0[k], mine1[k], false, false);
-            row[k] = sw[0];
-            row[2 + k] = sw[1];
-          }
-          __builtin_amdgcn_raw_buffer_store_b128(
-              row, orsrc,
-              (((16 * (2 * p2 + (odd ? 1 : 0)) + r16) * Hv + h) * V + 16 * (vt0 + sl) +
-               4 * (grp & 2)) * 2,
-              0, 0);
-        }
-      }
-    };
     if (kSplit && w == NS + 2) {
       // the save wave: chunk j-1's state and deltas during step j
       __syncthreads();
@@ -633,7 +478,7 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
       if (nc > 0) save_chunk(nc - 1, true);
       return;
     }
-    if constexpr (chain_split_out<SAVE, OUT, NS>()) {
+    if constexpr (OUT) {
       // ------------------------------------------- output waves (split) ----
       // Two output waves, each forming two of a chunk's four 16-row o tiles --
       // tiles 0 and 3 (role NS + 1) and tiles 1 and 2 (the last role), so that
@@ -812,56 +657,68 @@ chunk_chain_sw_kernel(const uint16_t* __restrict__ v, const uint16_t* __restrict
       };
       if (w == chain_waves<SAVE, OUT, NS, RAWK>() - 1) run(std::integral_constant<int, 1>{});
       else run(std::integral_constant<int, 0>{});
-      return;
-    }
-    // Every step issues its loads, then its stores (the o tiles, or without
-    // o the saves); the next step's wait leaves the previous step's stores
-    // and the current step's operations in flight, so each store has two
-    // steps to drain.  The prologue issues one such group per step before
-    // step 0 (loads for steps 0 and 1, stores dropped), so every wait of the
-    // loop names an exact count.
-    OutTile ot;
-    if (nc > 0) {
-      load_vg(rA, 0);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-      write_vg(rA, 0);
-      load_vg(rB, min(1, nc - 1));
-      if constexpr (OUT) out_store(ot, 0, false);
-      else save_chunk(0, false);
-      load_qp(rA, 0);
-      load_vg(rA, min(2, nc - 1));
-      if constexpr (OUT) out_store(ot, 0, false);
-      else save_chunk(0, false);
-    }
-    __syncthreads();
-    // step j works on register set (j + 1) % 2
-    auto step = [&](int j, Regs& r) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWait));   // chunk j-1's Q / P, chunk j+1's V / G
-      if (j + 1 < nc) write_vg(r, j + 1);
-      if constexpr (OUT) {
-        out_form(r, j - 1, j >= 1, ot);
-        load_qp(r, min(j + 1, nc - 1));
-        load_vg(r, min(j + 3, nc - 1));
-        out_store(ot, j - 1, j >= 1);
-      } else {
-        load_vg(r, min(j + 3, nc - 1));
-        if constexpr (SAVE) save_chunk(j - 1, j >= 1);
+    } else {
+      // During step j: writes chunk j+1's gate factors into stage buffer
+      // (j+1) % 3 and stores chunk j-1's saves (state and deltas), then loads
+      // chunk j+3's G into a register set loaded two steps before it is used
+      // (two sets, the loop unrolled by two); every step issues the same
+      // loads and stores, so each wait names an exact count.  The stores go
+      // after the step's load and the step's wait leaves the previous step's
+      // stores in flight too (the counter retires loads and stores in issue
+      // order): each store has two steps to drain.
+      constexpr int kSave = SAVE ? NS * (KB + 2) : 0;   // state and delta stores per chunk
+      constexpr int kWait = (kSave + 1) + kSave;
+      struct Regs {
+        float G;   // G of token `lane`
+      };
+      Regs rA, rB;
+      auto load_vg = [&](Regs& r, int j) {
+        const int ci = c_begin + j;
+        const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(ws.gate + ((size_t)ci * Hv + h) * 64), 0, 256, kBufferFlags);
+        r.G = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, lane * 4, 0, 0));
+      };
+      auto write_vg = [&](const Regs& r, int j) {
+        const int buf = j % 3;
+        const int t0 = s + j * kChunk, L = min(kChunk, e - t0);
+        const float GL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.G), L - 1));
+        const float eg = __expf(r.G);
+        Gst[buf][0][lane] = eg;
+        Gst[buf][1][lane] = __expf(GL - r.G);
+        if (lane == L - 1) Egl[buf] = eg;
+      };
+      // the prologue issues one such group per step before step 0 (loads for
+      // steps 0 and 1, stores dropped), so every wait of the loop names an
+      // exact count
+      if (nc > 0) {
+        load_vg(rA, 0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        write_vg(rA, 0);
+        load_vg(rB, min(1, nc - 1));
+        if constexpr (SAVE) save_chunk(0, false);
+        load_vg(rA, min(2, nc - 1));
+        if constexpr (SAVE) save_chunk(0, false);
       }
       __syncthreads();
-    };
-    int j = 0;
-    for (; j + 1 < nc; j += 2) {
-      step(j, rB);
-      step(j + 1, rA);
-    }
-    if (j < nc) step(j, rB);
-    if (nc > 0) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-      if constexpr (OUT) {
-        out_form((nc - 1) & 1 ? rB : rA, nc - 1, true, ot);
-        out_store(ot, nc - 1, true);
-      } else if constexpr (SAVE) {
-        save_chunk(nc - 1, true);
+      // step j works on register set (j + 1) % 2
+      auto step = [&](int j, Regs& r) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWait));   // chunk j+1's G
+        if (j + 1 < nc) write_vg(r, j + 1);
+        load_vg(r, min(j + 3, nc - 1));
+        if constexpr (SAVE) save_chunk(j - 1, j >= 1);
+        __syncthreads();
+      };
+      int j = 0;
+      for (; j + 1 < nc; j += 2) {
+        step(j, rB);
+        step(j + 1, rA);
+      }
+      if (j < nc) step(j, rB);
+      if constexpr (SAVE) {
+        if (nc > 0) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+          save_chunk(nc - 1, true);
+        }
       }
     }
   }
