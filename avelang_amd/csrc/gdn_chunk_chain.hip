@@ -731,8 +731,8 @@ void launch_chain_sw(const uint16_t* v, const uint16_t* qraw, const uint16_t* kr
                      hipStream_t st) {
   // two V tiles per workgroup once the chains fill the GPU twice over: the
   // tiles share the stage and output waves' operand traffic, and every chain
-  // still has a state wave of its own (not with both outputs: a fifth wave
-  // would halve the register budget; not with RAWK, see above)
+  // still has a state wave of its own (not with both outputs, where a save
+  // wave would make six waves; not with RAWK, see above)
   const long long chains = (long long)N * Hv * (V / 16);
   const bool rawq = OUT && qraw;
   const bool rawk = OUT && !SAVE && rawq && kraw;
