@@ -370,15 +370,19 @@ def test_decode_unit_key_retrieval_cfg2(rocm_device):
     assert (want - v).abs().max().item() <= 1e-5
 
 
-def test_prefill_l2norm_in_kernel(rocm_device):
+# (K, V, B): the l2norm form's chain reads the prep's fp16 Q fragments in its two
+# output waves; B = 8 gives 8 x 8 x V/16 chains, at least twice the CUs of an
+# MI355X for V = 128, so that case runs two V tiles per workgroup
+@pytest.mark.parametrize("K,V,B", [(128, 128, 1), (64, 64, 1), (128, 128, 8)])
+def test_prefill_l2norm_in_kernel(rocm_device, K, V, B):
     """In-kernel l2norm rounds the normalised q, k to bf16 (FLA's l2norm pass)."""
-    wl = W.make(1, 200, 4, 8, 128, 128, seed=88, h0_scale=0.01, l2norm=False)
+    wl = W.make(B, 200, 4, 8, K, V, seed=88 + K + B, h0_scale=0.01, l2norm=False)
     a = wl.numpy()
     nrm = lambda x: x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-6)  # noqa: E731
     a["q"], a["k"] = W._bf16_round(nrm(a["q"])), W._bf16_round(nrm(a["k"]))
     o_ref, s_ref = oracle.run("chunk", **a)
     o, s = _run_chunk(wl, rocm_device, use_qk_l2norm_in_kernel=True)
-    _check(o, o_ref, s, s_ref, "prefill l2norm")
+    _check(o, o_ref, s, s_ref, f"prefill l2norm K={K} V={V} B={B}")
 
 
 def test_golden_cfg0(rocm_device):
